@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the LayerAdam step on one MI355X.
+
+One step = the hot path over one Llama-3.1-8B decoder layer held flat in HBM
+(218,112,000 params): grad-norm stage 1 + 2, clip coefficient, then the fused
+AdamW + bf16-copy update, all through the product API
+(``LayerAdam.clip_grad_norm`` + ``LayerAdam.step_chunk``).  Inputs are resident
+in HBM before the timed region starts.
+
+Prints ONE JSON line (rank 0).  ``value`` = params / step time (Gparams/s).
+``roofline`` covers the dominant kernel (the update): algorithmic bytes = 28 B
+per param (read p4 g2 m4 v4, write p4 m4 v4 + bf16 copy 2) / its average
+duration measured with HIP events on its stream inside the timed region.
+``cpu_baseline`` times the reference CPU Adam (compiled from its own sources
+into oracle/_ref, or the C restatement in oracle/ when that is absent) on this
+host, on the same layer size.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "AdamW+bf16-cast Gparams/s & HBM GB/s (% of 8 TB/s), Llama-8B layer"
+PEAK_HBM_GBS = 8000.0
+BYTES_PER_PARAM_UPDATE = 28
+BYTES_PER_PARAM_NORM = 2
+LLAMA8B_LAYER = [4096 * 4096, 4096 * 1024, 4096 * 1024, 4096 * 4096, 4096 * 14336, 4096 * 14336,
+                 14336 * 4096, 4096, 4096]
+TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "la_adamw_kernel_c2_traffic.txt")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    """HBM bytes per update launch from the committed rocprofv3 --pmc summary, if any."""
+    try:
+        with open(TRAFFIC_SUMMARY) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(n: int, budget_s: float):
+    """Reference CPU Adam on this host: 28 B/param model, whole-layer steps
+    (methodology of bench/cpu_adam_profile/cpu_adam_benchmark.py:392-428)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    ref = O.load_ref()
+    kind = "reference" if ref is not None else "port"
+    p = torch.randn(n) * 0.02
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    g = (torch.randn(n) * 1e-3).bfloat16()
+    staging = torch.empty(n, dtype=torch.bfloat16)
+    if ref is not None:
+        ref.create_adam(0, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
+
+        def step(t):
+            ref.adam_update(0, t, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v)
+    else:
+        orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+        pn, mn, vn = p.numpy(), m.numpy(), v.numpy()
+        gn = g.view(torch.int16).numpy().view(np.uint16)
+
+        def step(t):
+            orc.update(t, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, pn, gn, mn, vn, g16="bf16")
+    t = 0
+    for _ in range(2):
+        t += 1
+        step(t)
+    times, cast_times = [], []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 20 and (time.perf_counter() < t_end or len(times) < 3):
+        t += 1
+        t0 = time.perf_counter()
+        step(t)
+        t1 = time.perf_counter()
+        staging.copy_(p)  # the runtime's fp32 -> bf16 cast, transformer_layer.py:304
+        t2 = time.perf_counter()
+        times.append(t1 - t0)
+        cast_times.append(t2 - t1)
+    adam_s = sum(times) / len(times)
+    cast_s = sum(cast_times) / len(cast_times)
+    return {
+        "value": round(n / (adam_s + cast_s) / 1e9, 4),
+        "unit": "Gparams/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"{len(times)} whole-layer steps of {n} params (AdamW, fp32 p/m/v, bf16 grads) "
+                   f"+ torch fp32->bf16 copy_, {threads} OpenMP threads on "
+                   f"{os.cpu_count()} visible CPUs"),
+        "adam_only_gparams_s": round(n / adam_s / 1e9, 4),
+        "adam_ms": round(adam_s * 1e3, 3),
+        "cast_ms": round(cast_s * 1e3, 3),
+        "gbs_28B": round(n * 28 / adam_s / 1e9, 2),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU-baseline timing (0 disables it)")
+    ap.add_argument("--no-clip", action="store_true", help="time the update alone (no norm pass)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
+              "(the LayerAdam step is elementwise and would shard by contiguous slices; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from slideformer_amd import LayerAdam
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = sum(LLAMA8B_LAYER)
+    log(f"device {torch.cuda.get_device_name(dev)}; C2 layer n={n}")
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20)
+    p = torch.randn(n, generator=gen, device=dev) * 0.02
+    m = torch.zeros(n, device=dev)
+    v = torch.zeros(n, device=dev)
+    g = (torch.randn(n, generator=gen, device=dev) * 1e-3).bfloat16()
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    adam = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    stream = torch.cuda.current_stream(dev)
+    clip = not args.no_clip
+
+    def one_step(t, ev=None):
+        group = dict(adam.defaults, step=t)
+        coef = None
+        if clip:
+            coef, _ = adam.clip_grad_norm([g], 1.0, stream=stream)
+        if ev is not None:
+            ev[0].record(stream)
+        adam.step_chunk(p, g, m, v, group, bf16_out=out, clip_coef=coef, stream=stream)
+        if ev is not None:
+            ev[1].record(stream)
+
+    # m/v warmed by 5 prior steps (config C2), then the untimed warm-up steps
+    t = 0
+    for _ in range(5 + args.warmup):
+        t += 1
+        one_step(t)
+    torch.cuda.synchronize()
+    log(f"warm-up done ({5 + args.warmup} steps)")
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(args.steps):
+        t += 1
+        one_step(t, evs[i])
+    stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    ms_per_step = total_ms / args.steps
+    upd_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    upd_avg = sum(upd_ms) / len(upd_ms)
+    log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, update kernel avg {upd_avg:.4f} ms "
+        f"(min {upd_ms[0]:.4f}, max {upd_ms[-1]:.4f})")
+
+    value = n / (ms_per_step * 1e-3) / 1e9
+    achieved = BYTES_PER_PARAM_UPDATE * n / (upd_avg * 1e-3) / 1e9
+    step_bytes = (BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0)) * n
+    traffic = read_traffic()
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) fp32 master, N(0,1e-3) bf16 grads, resident in HBM)",
+        "config": {
+            "workload": ("C2: one Llama-3.1-8B decoder layer, flat, 218,112,000 params resident in HBM; "
+                         "grad-norm clip at 1.0 + fused AdamW (lr 1e-5, betas 0.9/0.999, eps 1e-8, "
+                         "wd 0.01) + bf16 compute copy" if clip else
+                         "C2 layer, fused AdamW + bf16 copy only (no norm pass)"),
+            "params": n,
+            "grad_dtype": "bf16",
+            "state_dtype": "f32",
+            "bytes_per_param_step": BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0),
+        },
+        "hbm_gbs_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "hbm_frac_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "update_kernel_ms": round(upd_avg, 4),
+        "update_gparams_s": round(n / (upd_avg * 1e-3) / 1e9, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "kernel": "la_adamw_kernel<float, bf16_t, float>",
+            "algorithmic_bytes_per_launch": BYTES_PER_PARAM_UPDATE * n,
+        },
+        "cpu_baseline": None,
+    }
+    if args.cpu_budget > 0:
+        del p, m, v, g, out
+        torch.cuda.empty_cache()
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(n, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

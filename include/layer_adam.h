@@ -1,0 +1,127 @@
+/*
+ * slideformer_amd -- C-ABI of the MI355X (gfx950) LayerAdam step.
+ *
+ * Replaces the reference's pybind module `cpu_adam`
+ * (optimizer/layer_adam/csrc/cpu_adam.cpp:8-13, declarations cpu_adam.h:199-221).
+ * Plain pointers and sizes only; no torch types.  The caller owns every buffer;
+ * the library keeps only per-id scalar state (the beta-power state machine).
+ *
+ * Return codes: 0 on success; LA_EINVAL for a null/misaligned pointer, an
+ * unknown id or a bad size; LA_EDTYPE for a dtype triple the reference does
+ * not register; a positive hipError_t value when a HIP call fails.
+ * All device entry points are asynchronous on the stream passed in.
+ */
+#ifndef SLIDEFORMER_AMD_LAYER_ADAM_H
+#define SLIDEFORMER_AMD_LAYER_ADAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LA_ABI_VERSION 1
+
+#define LA_OK 0
+#define LA_EINVAL (-22)
+#define LA_EDTYPE (-95)
+
+/* element types of p / g / m,v */
+#define LA_F32 0
+#define LA_BF16 1
+#define LA_F16 2
+
+/* opaque HIP stream (hipStream_t); NULL = the default stream */
+typedef void* la_stream_t;
+
+/*
+ * Scalars of one adam_update call, derived on the host by la_scalars()
+ * exactly as Adam_Optimizer::IncrementStep + update_state + Step_AVX do
+ * (cpu_adam.h:57-89, :131-148).
+ */
+typedef struct {
+    float beta1, beta2;              /* _betta1, _betta2 */
+    float one_minus_beta1;           /* 1 - b1            cpu_adam.h:131 */
+    float one_minus_beta2;           /* 1 - b2            cpu_adam.h:132 */
+    float bias_correction2;          /* 1/sqrtf(1-b2^t) or 1 (cpu_adam.h:87) */
+    float eps;                       /* _eps */
+    float step_size;                 /* -lr / bc1         cpu_adam.h:142 */
+    float w_decay;                   /* -lr * wd          cpu_adam.h:146 */
+    float weight_decay;              /* wd (L2 mode)      cpu_adam.h:148 */
+    int32_t decay_mode;              /* 0 none, 1 L2 into the grad, 2 decoupled (AdamW) */
+    float beta1_t, beta2_t;          /* _betta1_t, _betta2_t after IncrementStep */
+    float bias_correction1;          /* 1 - b1^t or 1 */
+    uint64_t step;                   /* _step after IncrementStep */
+} la_scalars_t;
+
+/* ABI version (LA_ABI_VERSION) */
+int la_abi_version(void);
+
+/* Human-readable text for a return code. */
+const char* la_strerror(int code);
+
+/*
+ * Create / reset scalar state for `id`.
+ * Replaces create_adam_optimizer, cpu_adam_impl.cpp:91-129 (pybind create_adam).
+ * adamw_mode is fixed here, as in the reference; lr/eps/wd/betas are per call.
+ */
+int la_create(int id, float lr, float beta1, float beta2, float eps, float weight_decay,
+              int adamw_mode, int should_log);
+
+/* Replaces destroy_adam_optimizer, cpu_adam_impl.cpp:272-277 (pybind destroy_adam). */
+int la_destroy(int id);
+
+/*
+ * Advance the beta-power state machine of `id` for one adam_update call and
+ * return the derived scalars (cpu_adam.h:57-89; called at cpu_adam_impl.cpp:241-242).
+ * Mutates the per-id state exactly like one reference call.
+ */
+int la_scalars(int id, uint64_t step, float lr, float beta1, float beta2, float eps,
+               float weight_decay, int bias_correction, la_scalars_t* out);
+
+/*
+ * The fused elementwise update on device buffers, in place:
+ *   p, m, v updated (Step_AVX body, cpu_adam.h:159-192; the last n % 16
+ *   elements follow the reference's scalar tail, cpu_adam_impl.cpp:46-67),
+ *   p_bf16_out[i] = RNE bf16 of the new p (nullable; transformer_layer.py:302-305),
+ *   grads scaled by *clip_coef before use (nullable device pointer).
+ * Elementwise body of ds_adam_step, cpu_adam_impl.cpp:255-267 (Step_8 cascade).
+ */
+int la_adamw_step(const la_scalars_t* sc, int p_dtype, void* p, int g_dtype, const void* g,
+                  int s_dtype, void* m, void* v, uint64_t n, uint16_t* p_bf16_out,
+                  const float* clip_coef, la_stream_t stream);
+
+/*
+ * One whole reference call: la_scalars + la_adamw_step.
+ * Replaces ds_adam_step, cpu_adam_impl.cpp:220-270 (pybind adam_update).
+ */
+int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, int bias_correction, int p_dtype, void* p, int g_dtype,
+                   const void* g, int s_dtype, void* m, void* v, uint64_t n,
+                   uint16_t* p_bf16_out, const float* clip_coef, la_stream_t stream);
+
+/*
+ * Grad-norm stage 1 + 2 (no counterpart in the reference, which has no
+ * clipping; SlideFormer's update sits at transformer_layer.py:453-493):
+ * sum of squares of g[0..n) in float64 into *sqnorm (device), added to the
+ * old value when accumulate != 0.  `partials` is a caller-owned device
+ * workspace of at least la_grad_sqnorm_workspace(n) bytes.
+ * Deterministic for a given n and pointer alignment.
+ */
+uint64_t la_grad_sqnorm_workspace(uint64_t n);
+int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, double* partials,
+                   uint64_t partials_bytes, double* sqnorm, int accumulate, la_stream_t stream);
+
+/*
+ * Clip coefficient on device, torch.nn.utils.clip_grad_norm_ convention:
+ * norm = (float)sqrt(*sqnorm); *coef = min(1, max_norm / (norm + 1e-6)) in fp32;
+ * *norm_out = norm (nullable).  No host synchronisation.
+ */
+int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out,
+                 la_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SLIDEFORMER_AMD_LAYER_ADAM_H */

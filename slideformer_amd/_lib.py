@@ -1,0 +1,110 @@
+"""ctypes binding of ``libslideformer_amd.so`` (C-ABI declared in ``include/layer_adam.h``).
+
+The library is loaded after ``import torch`` so that it binds to the HIP runtime
+torch already loaded (both carry the soname ``libamdhip64.so.7``); device
+pointers and streams from torch are then valid in it.
+
+There is no fallback: if the library is missing, ``load()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (binds the HIP runtime before the library is loaded)
+
+from .build import LIB_PATH
+
+LA_OK = 0
+LA_EINVAL = -22
+LA_EDTYPE = -95
+
+LA_F32, LA_BF16, LA_F16 = 0, 1, 2
+
+# every exported symbol of include/layer_adam.h
+EXPORTED = (
+    "la_abi_version",
+    "la_strerror",
+    "la_create",
+    "la_destroy",
+    "la_scalars",
+    "la_adamw_step",
+    "la_adam_update",
+    "la_grad_sqnorm_workspace",
+    "la_grad_sqnorm",
+    "la_clip_coef",
+)
+
+
+class LaScalars(ctypes.Structure):
+    """Mirror of ``la_scalars_t``."""
+
+    _fields_ = [
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("one_minus_beta1", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("bias_correction2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("step_size", ctypes.c_float),
+        ("w_decay", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("decay_mode", ctypes.c_int32),
+        ("beta1_t", ctypes.c_float),
+        ("beta2_t", ctypes.c_float),
+        ("bias_correction1", ctypes.c_float),
+        ("step", ctypes.c_uint64),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(L):
+    P = ctypes.c_void_p
+    f, i, u64 = ctypes.c_float, ctypes.c_int, ctypes.c_uint64
+    SP = ctypes.POINTER(LaScalars)
+    L.la_abi_version.argtypes = []
+    L.la_abi_version.restype = i
+    L.la_strerror.argtypes = [i]
+    L.la_strerror.restype = ctypes.c_char_p
+    L.la_create.argtypes = [i, f, f, f, f, f, i, i]
+    L.la_create.restype = i
+    L.la_destroy.argtypes = [i]
+    L.la_destroy.restype = i
+    L.la_scalars.argtypes = [i, u64, f, f, f, f, f, i, SP]
+    L.la_scalars.restype = i
+    L.la_adamw_step.argtypes = [SP, i, P, i, P, i, P, P, u64, P, P, P]
+    L.la_adamw_step.restype = i
+    L.la_adam_update.argtypes = [i, u64, f, f, f, f, f, i, i, P, i, P, i, P, P, u64, P, P, P]
+    L.la_adam_update.restype = i
+    L.la_grad_sqnorm_workspace.argtypes = [u64]
+    L.la_grad_sqnorm_workspace.restype = u64
+    L.la_grad_sqnorm.argtypes = [i, P, u64, P, u64, P, i, P]
+    L.la_grad_sqnorm.restype = i
+    L.la_clip_coef.argtypes = [P, f, P, P, P]
+    L.la_clip_coef.restype = i
+    return L
+
+
+def load(path: str | None = None):
+    """Load the HIP library (once).  Raises ImportError if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = path or os.environ.get("SLIDEFORMER_AMD_LIB", LIB_PATH)
+        if not os.path.exists(path):
+            raise ImportError(
+                f"slideformer_amd HIP library not found at {path}; build it with "
+                "`python -m slideformer_amd.build` (there is no CPU fallback)")
+        _lib = _declare(ctypes.CDLL(path))
+        return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != LA_OK:
+        msg = load().la_strerror(rc).decode()
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,67 @@
+"""Build recipe for the in-tree HIP library ``slideformer_amd/lib/libslideformer_amd.so``.
+
+Usage: ``python -m slideformer_amd.build`` (also called by ``__graft_entry__.build()``).
+
+The library is one HIP translation unit compiled for gfx950 only.  Flags:
+  -ffp-contract=off       every FMA in the kernels is an explicit fmaf(), so the
+                          op order matches the reference CPU Adam exactly;
+  no fast-math flags      fp32 division and sqrt stay correctly rounded and
+                          denormals are kept;
+  -packed-fp32-ops off    no v_pk_{add,mul,fma}_f32 in the generated code.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_NAME = "libslideformer_amd.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+SOURCES = [os.path.join(CSRC, "layer_adam.hip")]
+ARCH = "gfx950"
+
+BASE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the HIP library cannot be built")
+
+
+def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: bool = False) -> str:
+    """Compile the library for gfx950 into ``out`` (atomically replaced)."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *BASE_FLAGS]
+    for k, v in (defines or {}).items():
+        cmd.append(f"-D{k}={v}")
+    cmd += ["-I", os.path.join(REPO_DIR, "include"), "-o", tmp, *SOURCES]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with code {res.returncode}")
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

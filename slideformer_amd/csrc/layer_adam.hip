@@ -1,0 +1,670 @@
+// slideformer_amd: fused LayerAdam step for MI355X (gfx950, wave64).
+//
+// One pass over a layer's flat buffers reads p, g, m, v and writes p, m, v and
+// the bf16 compute copy of p: 28 algorithmic bytes per element for the hot
+// triple (fp32 p/m/v, bf16 g).  Nothing here is a contraction, so there is no
+// MFMA; the kernel is bound by HBM bandwidth.  Each lane moves 8 consecutive
+// elements per iteration with 16-byte global loads/stores.
+//
+// Arithmetic follows the reference CPU Adam op for op (cpu_adam.h:159-192),
+// with explicit fmaf() and this file compiled with -ffp-contract=off; fp32
+// division and sqrt stay correctly rounded (no fast-math flags), denormals are
+// kept.  The last n % 16 elements of a call follow the reference's scalar tail
+// (cpu_adam_impl.cpp:46-67) as its GCC build contracts it.
+//
+// The grad norm is a two-stage reduction: per-lane float64 sums, a wave64 DPP
+// reduction, LDS across the 4 waves of a workgroup, one partial per workgroup,
+// then a single workgroup folds the partials in a fixed order.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/layer_adam.h"
+
+#ifndef LA_BLOCK
+#define LA_BLOCK 256
+#endif
+// Upper bound on update workgroups per launch (grid-stride beyond it).
+#ifndef LA_MAX_GRID
+#define LA_MAX_GRID 8192
+#endif
+// Workgroups of the grad-norm stage 1 (bounded so stage 2 is one workgroup).
+#ifndef LA_NORM_MAX_GRID
+#define LA_NORM_MAX_GRID 2048
+#endif
+// Groups of 8 elements each lane handles per loop trip.
+#ifndef LA_UNROLL
+#define LA_UNROLL 1
+#endif
+
+namespace {
+
+constexpr int kVec = 8;  // elements per lane per group
+
+// ---------------------------------------------------------------------------
+// element types
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t x; };
+struct f16_t { uint16_t x; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// RNE with NaN -> 0x7FC0, the reference's bf16 store (simd.h:56-86) and c10's
+// round_to_nearest_even used by the fp32->bf16 copy_ (transformer_layer.py:304).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
+{
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f)
+{
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <typename T> struct Io;
+
+template <> struct Io<float> {
+    static constexpr int kBytes = 4;
+    __device__ __forceinline__ static void load8(const void* base, uint64_t e, float (&x)[kVec])
+    {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(base) + e);
+        float4 a = q[0], b = q[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+    __device__ __forceinline__ static void store8(void* base, uint64_t e, const float (&x)[kVec])
+    {
+        float4* q = reinterpret_cast<float4*>(static_cast<float*>(base) + e);
+        q[0] = make_float4(x[0], x[1], x[2], x[3]);
+        q[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
+    __device__ __forceinline__ static float load1(const void* base, uint64_t e)
+    {
+        return static_cast<const float*>(base)[e];
+    }
+    __device__ __forceinline__ static void store1(void* base, uint64_t e, float x)
+    {
+        static_cast<float*>(base)[e] = x;
+    }
+};
+
+template <typename Conv> struct Io16 {
+    static constexpr int kBytes = 2;
+    __device__ __forceinline__ static void load8(const void* base, uint64_t e, float (&x)[kVec])
+    {
+        uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + e);
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = Conv::to_f32(w[j] & 0xffffu);
+            x[2 * j + 1] = Conv::to_f32(w[j] >> 16);
+        }
+    }
+    __device__ __forceinline__ static void store8(void* base, uint64_t e, const float (&x)[kVec])
+    {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = Conv::from_f32(x[2 * j]) | (Conv::from_f32(x[2 * j + 1]) << 16);
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + e) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    __device__ __forceinline__ static float load1(const void* base, uint64_t e)
+    {
+        return Conv::to_f32(static_cast<const uint16_t*>(base)[e]);
+    }
+    __device__ __forceinline__ static void store1(void* base, uint64_t e, float x)
+    {
+        static_cast<uint16_t*>(base)[e] = static_cast<uint16_t>(Conv::from_f32(x));
+    }
+};
+
+struct ConvBf16 {
+    __device__ __forceinline__ static float to_f32(uint32_t h) { return bf16_bits_to_f32(h); }
+    __device__ __forceinline__ static uint32_t from_f32(float f) { return f32_to_bf16_bits(f); }
+};
+struct ConvF16 {
+    __device__ __forceinline__ static float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
+    __device__ __forceinline__ static uint32_t from_f32(float f) { return f32_to_f16_bits(f); }
+};
+template <> struct Io<bf16_t> : Io16<ConvBf16> {};
+template <> struct Io<f16_t> : Io16<ConvF16> {};
+
+// ---------------------------------------------------------------------------
+// the element update
+// ---------------------------------------------------------------------------
+struct Coeffs {
+    float b1, b2, omb1, omb2, bc2, eps, step_size, w_decay, wd;
+    int32_t mode;  // 0 none, 1 L2, 2 decoupled
+};
+
+// SIMD body order of the reference, cpu_adam.h:159-192.
+__device__ __forceinline__ void adam_body(float& p, float g, float& m, float& v, const Coeffs& k)
+{
+    if (k.mode == 1) g = __builtin_fmaf(p, k.wd, g);          // :171-173
+    m = m * k.b1;                                            // :175
+    m = __builtin_fmaf(g, k.omb1, m);                        // :176
+    v = v * k.b2;                                            // :177
+    float gg = g * g;                                        // :178
+    v = __builtin_fmaf(gg, k.omb2, v);                       // :179
+    float d = __builtin_sqrtf(v);                            // :180
+    d = __builtin_fmaf(d, k.bc2, k.eps);                     // :181
+    float u = m / d;                                         // :182
+    if (k.mode == 2) p = __builtin_fmaf(p, k.w_decay, p);    // :184-186
+    p = __builtin_fmaf(u, k.step_size, p);                   // :188
+}
+
+// Scalar tail of the reference, cpu_adam_impl.cpp:46-67, as GCC -O3 with an
+// FMA ISA contracts it: the m*b1 and v*b2 products are the fused ones.
+__device__ __forceinline__ void adam_tail(float& p, float g, float& m, float& v, const Coeffs& k)
+{
+    if (k.mode == 1) g = __builtin_fmaf(p, k.wd, g);
+    float gm = g * k.omb1;
+    m = __builtin_fmaf(m, k.b1, gm);
+    float gg = g * g;
+    gg = gg * k.omb2;
+    v = __builtin_fmaf(v, k.b2, gg);
+    float d = __builtin_sqrtf(v);
+    d = __builtin_fmaf(d, k.bc2, k.eps);
+    float u = m / d;
+    if (k.mode == 2) p = __builtin_fmaf(p, k.w_decay, p);
+    p = __builtin_fmaf(u, k.step_size, p);
+}
+
+struct StepArgs {
+    void* p;
+    const void* g;
+    void* m;
+    void* v;
+    uint16_t* out;       // bf16 compute copy, may be null
+    const float* coef;   // clip coefficient (device), may be null
+    uint64_t n;
+    uint64_t head;       // elements before the first aligned group
+    uint64_t nvec;       // aligned groups of 8, starting at `head`
+    uint64_t tail_start; // n - n % 16: first element of the reference's scalar tail
+    Coeffs k;
+};
+
+template <typename TP, typename TG, typename TS>
+__global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
+{
+    const bool has_coef = a.coef != nullptr;
+    const float coef = has_coef ? *a.coef : 1.0f;
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
+
+    for (uint64_t base = tid; base < a.nvec; base += stride * LA_UNROLL) {
+        float p[LA_UNROLL][kVec], g[LA_UNROLL][kVec], m[LA_UNROLL][kVec], v[LA_UNROLL][kVec];
+        bool live[LA_UNROLL];
+#pragma unroll
+        for (int u = 0; u < LA_UNROLL; ++u) {
+            const uint64_t gi = base + u * stride;
+            live[u] = gi < a.nvec;
+            if (live[u]) {
+                const uint64_t e = a.head + gi * kVec;
+                Io<TG>::load8(a.g, e, g[u]);
+                Io<TP>::load8(a.p, e, p[u]);
+                Io<TS>::load8(a.m, e, m[u]);
+                Io<TS>::load8(a.v, e, v[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < LA_UNROLL; ++u) {
+            if (!live[u]) continue;
+            const uint64_t e = a.head + (base + u * stride) * kVec;
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                float gj = has_coef ? g[u][j] * coef : g[u][j];
+                adam_body(p[u][j], gj, m[u][j], v[u][j], a.k);
+            }
+            Io<TP>::store8(a.p, e, p[u]);
+            Io<TS>::store8(a.m, e, m[u]);
+            Io<TS>::store8(a.v, e, v[u]);
+            if (a.out) Io<bf16_t>::store8(a.out, e, p[u]);
+        }
+    }
+
+    // Elements outside the aligned groups: [0, head) and [head + 8*nvec, n).
+    const uint64_t vec_end = a.head + a.nvec * kVec;
+    const uint64_t nscalar = a.head + (a.n - vec_end);
+    for (uint64_t s = tid; s < nscalar; s += stride) {
+        const uint64_t e = s < a.head ? s : vec_end + (s - a.head);
+        float g = Io<TG>::load1(a.g, e);
+        if (has_coef) g = g * coef;
+        float p = Io<TP>::load1(a.p, e);
+        float m = Io<TS>::load1(a.m, e);
+        float v = Io<TS>::load1(a.v, e);
+        if (e >= a.tail_start) adam_tail(p, g, m, v, a.k);
+        else adam_body(p, g, m, v, a.k);
+        Io<TP>::store1(a.p, e, p);
+        Io<TS>::store1(a.m, e, m);
+        Io<TS>::store1(a.v, e, v);
+        if (a.out) a.out[e] = static_cast<uint16_t>(f32_to_bf16_bits(p));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grad norm
+// ---------------------------------------------------------------------------
+
+// Move a float64 across lanes with one DPP control on both 32-bit halves.
+// Rows disabled by ROW_MASK read 0.0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double x)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), CTRL,
+                                               ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)),
+                                               CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                          static_cast<uint32_t>(lo));
+}
+
+// wave64 sum; the total lands in lane 63.  Fixed order, so deterministic.
+__device__ __forceinline__ double wave_sum_f64(double x)
+{
+    x += dpp_f64<0xb1>(x);        // quad_perm [1,0,3,2]
+    x += dpp_f64<0x4e>(x);        // quad_perm [2,3,0,1]
+    x += dpp_f64<0x141>(x);       // row_half_mirror: 8-lane sums
+    x += dpp_f64<0x140>(x);       // row_mirror: 16-lane (row) sums
+    x += dpp_f64<0x142, 0xa>(x);  // row_bcast15 into rows 1 and 3
+    x += dpp_f64<0x143, 0xc>(x);  // row_bcast31 into rows 2 and 3
+    return x;
+}
+
+// Sum over the workgroup; valid in thread 0.
+__device__ __forceinline__ double block_sum_f64(double x)
+{
+    __shared__ double part[LA_BLOCK / 64];
+    x = wave_sum_f64(x);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 63) part[wave] = x;
+    __syncthreads();
+    double t = 0.0;
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < LA_BLOCK / 64; ++w) t += part[w];
+    }
+    return t;
+}
+
+template <typename TG>
+__global__ __launch_bounds__(LA_BLOCK) void la_sqnorm_stage1(const void* g, uint64_t n, uint64_t head,
+                                                             uint64_t nvec, double* partials)
+{
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
+    double acc = 0.0;
+    for (uint64_t gi = tid; gi < nvec; gi += stride) {
+        float x[kVec];
+        Io<TG>::load8(g, head + gi * kVec, x);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+            const double d = static_cast<double>(x[j]);
+            acc = __builtin_fma(d, d, acc);
+        }
+    }
+    const uint64_t vec_end = head + nvec * kVec;
+    const uint64_t nscalar = head + (n - vec_end);
+    for (uint64_t s = tid; s < nscalar; s += stride) {
+        const uint64_t e = s < head ? s : vec_end + (s - head);
+        const double d = static_cast<double>(Io<TG>::load1(g, e));
+        acc = __builtin_fma(d, d, acc);
+    }
+    const double t = block_sum_f64(acc);
+    if (threadIdx.x == 0) partials[blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(LA_BLOCK) void la_sqnorm_stage2(const double* partials, uint32_t count,
+                                                             double* sqnorm, int accumulate)
+{
+    double acc = 0.0;
+    for (uint32_t i = threadIdx.x; i < count; i += LA_BLOCK) acc += partials[i];
+    const double t = block_sum_f64(acc);
+    if (threadIdx.x == 0) *sqnorm = accumulate ? *sqnorm + t : t;
+}
+
+__global__ void la_clip_coef_kernel(const double* sqnorm, float max_norm, float* coef, float* norm_out)
+{
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const float norm = static_cast<float>(__builtin_sqrt(*sqnorm));
+    const float c = max_norm / (norm + 1e-6f);
+    *coef = (c < 1.0f || c != c) ? c : 1.0f;
+    if (norm_out) *norm_out = norm;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+// Scalar state of one optimizer id, Adam_Optimizer members cpu_adam.h:91-105.
+struct HostState {
+    float alpha, betta1, betta2, eps, weight_decay;
+    float betta1_t = 1.0f, betta2_t = 1.0f;
+    uint64_t step = 0;
+    float bias_correction1 = 1.0f, bias_correction2 = 1.0f;
+    bool adamw_mode = true;
+};
+
+std::mutex g_mu;
+std::unordered_map<int, HostState> g_states;
+
+int elem_bytes(int dt) { return dt == LA_F32 ? 4 : 2; }
+bool dt_valid(int dt) { return dt == LA_F32 || dt == LA_BF16 || dt == LA_F16; }
+
+// The nine (param, grad, state) triples the reference registers,
+// cpu_adam_impl.cpp:181-189.
+bool triple_registered(int p, int g, int s)
+{
+    if (p == LA_F32) return s == LA_F32;                                   // (f32, f32|bf16|f16, f32)
+    if (p == LA_BF16) return g != LA_F16 && (s == LA_F32 || (s == LA_BF16 && g == LA_BF16));
+    /* p == LA_F16 */ return g != LA_BF16 && (s == LA_F32 || (s == LA_F16 && g == LA_F16));
+}
+
+// First element index h in [0, 8) at which every pointer is 16-byte aligned,
+// or -1 when the pointers disagree in phase.
+int common_head(const uintptr_t* addr, const int* bytes, int count)
+{
+    for (int h = 0; h < kVec; ++h) {
+        bool ok = true;
+        for (int i = 0; i < count && ok; ++i) ok = ((addr[i] + static_cast<uintptr_t>(h) * bytes[i]) & 15u) == 0;
+        if (ok) return h;
+    }
+    return -1;
+}
+
+int g_cu_count = 0;
+
+int cu_count()
+{
+    if (g_cu_count > 0) return g_cu_count;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    g_cu_count = cus;
+    return cus;
+}
+
+uint32_t update_grid(uint64_t work)
+{
+    uint64_t blocks = (work + LA_BLOCK - 1) / LA_BLOCK;
+    if (blocks < 1) blocks = 1;
+    if (blocks > LA_MAX_GRID) blocks = LA_MAX_GRID;
+    return static_cast<uint32_t>(blocks);
+}
+
+uint32_t norm_grid(uint64_t n)
+{
+    const uint64_t groups = (n + kVec - 1) / kVec;
+    uint64_t blocks = (groups + LA_BLOCK - 1) / LA_BLOCK;
+    if (blocks < 1) blocks = 1;
+    if (blocks > LA_NORM_MAX_GRID) blocks = LA_NORM_MAX_GRID;
+    return static_cast<uint32_t>(blocks);
+}
+
+int hip_rc(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
+
+template <typename TP, typename TG, typename TS>
+int launch_step(const StepArgs& a, hipStream_t stream)
+{
+    const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
+    const uint64_t work = a.nvec > nscalar ? (a.nvec + LA_UNROLL - 1) / LA_UNROLL : nscalar;
+    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(update_grid(work)), dim3(LA_BLOCK), 0, stream, a);
+    return hip_rc(hipGetLastError());
+}
+
+template <typename TP, typename TG>
+int dispatch_s(int s_dt, const StepArgs& a, hipStream_t st)
+{
+    switch (s_dt) {
+    case LA_F32: return launch_step<TP, TG, float>(a, st);
+    case LA_BF16: return launch_step<TP, TG, bf16_t>(a, st);
+    default: return launch_step<TP, TG, f16_t>(a, st);
+    }
+}
+
+template <typename TP>
+int dispatch_g(int g_dt, int s_dt, const StepArgs& a, hipStream_t st)
+{
+    switch (g_dt) {
+    case LA_F32: return dispatch_s<TP, float>(s_dt, a, st);
+    case LA_BF16: return dispatch_s<TP, bf16_t>(s_dt, a, st);
+    default: return dispatch_s<TP, f16_t>(s_dt, a, st);
+    }
+}
+
+void derive_scalars(HostState& s, uint64_t step, float lr, float b1, float b2, float eps, float wd,
+                    int bias_correction, la_scalars_t* out)
+{
+    // IncrementStep, cpu_adam.h:57-76; std::pow(float, size_t) is a double pow.
+    if (b1 != s.betta1 || b2 != s.betta2) {
+        s.step = step;
+        s.betta1 = b1;
+        s.betta2 = b2;
+        s.betta1_t = static_cast<float>(std::pow(static_cast<double>(s.betta1), static_cast<double>(step)));
+        s.betta2_t = static_cast<float>(std::pow(static_cast<double>(s.betta2), static_cast<double>(step)));
+    } else {
+        s.step++;
+        if (s.step != step) {
+            s.betta1_t = static_cast<float>(std::pow(static_cast<double>(s.betta1), static_cast<double>(step)));
+            s.betta2_t = static_cast<float>(std::pow(static_cast<double>(s.betta2), static_cast<double>(step)));
+            s.step = step;
+        } else {
+            s.betta1_t *= s.betta1;
+            s.betta2_t *= s.betta2;
+        }
+    }
+    // update_state, cpu_adam.h:77-89 (float sqrt and float divide).
+    s.alpha = lr;
+    s.eps = eps;
+    s.weight_decay = wd;
+    s.bias_correction1 = 1.0f;
+    s.bias_correction2 = 1.0f;
+    if (bias_correction) {
+        s.bias_correction1 = 1.0f - s.betta1_t;
+        s.bias_correction2 = 1.0f / std::sqrt(1.0f - s.betta2_t);
+    }
+    // Step_AVX prologue, cpu_adam.h:131-148.
+    out->beta1 = s.betta1;
+    out->beta2 = s.betta2;
+    out->one_minus_beta1 = 1.0f - s.betta1;
+    out->one_minus_beta2 = 1.0f - s.betta2;
+    out->bias_correction2 = s.bias_correction2;
+    out->eps = s.eps;
+    out->step_size = -1.0f * s.alpha / s.bias_correction1;
+    out->w_decay = -1.0f * s.alpha * s.weight_decay;
+    out->weight_decay = s.weight_decay;
+    out->decay_mode = s.weight_decay > 0.0f ? (s.adamw_mode ? 2 : 1) : 0;
+    out->beta1_t = s.betta1_t;
+    out->beta2_t = s.betta2_t;
+    out->bias_correction1 = s.bias_correction1;
+    out->step = s.step;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int la_abi_version(void) { return LA_ABI_VERSION; }
+
+const char* la_strerror(int code)
+{
+    if (code == LA_OK) return "ok";
+    if (code == LA_EINVAL) return "invalid argument (null/misaligned pointer, unknown id or bad size)";
+    if (code == LA_EDTYPE) return "dtype triple not supported";
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown error";
+}
+
+int la_create(int id, float lr, float beta1, float beta2, float eps, float weight_decay, int adamw_mode,
+              int should_log)
+{
+    HostState s;
+    s.alpha = lr;
+    s.betta1 = beta1;
+    s.betta2 = beta2;
+    s.eps = eps;
+    s.weight_decay = weight_decay;
+    s.adamw_mode = adamw_mode != 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_states[id] = s;
+    }
+    if (should_log) {
+        std::printf("Adam Optimizer #%d is created with MI355X (gfx950 HIP) arithmetic capability.\n", id);
+        std::printf("Config: alpha=%f, betas=(%f, %f), weight_decay=%f, adam_w=%d\n", lr, beta1, beta2,
+                    weight_decay, adamw_mode ? 1 : 0);
+    }
+    return LA_OK;
+}
+
+int la_destroy(int id)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_states.erase(id);
+    return LA_OK;
+}
+
+int la_scalars(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
+               int bias_correction, la_scalars_t* out)
+{
+    if (!out) return LA_EINVAL;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_states.find(id);
+    if (it == g_states.end()) return LA_EINVAL;
+    derive_scalars(it->second, step, lr, beta1, beta2, eps, weight_decay, bias_correction, out);
+    return LA_OK;
+}
+
+int la_adamw_step(const la_scalars_t* sc, int p_dtype, void* p, int g_dtype, const void* g, int s_dtype,
+                  void* m, void* v, uint64_t n, uint16_t* p_bf16_out, const float* clip_coef,
+                  la_stream_t stream)
+{
+    if (!sc) return LA_EINVAL;
+    if (!dt_valid(p_dtype) || !dt_valid(g_dtype) || !dt_valid(s_dtype)) return LA_EDTYPE;
+    if (!triple_registered(p_dtype, g_dtype, s_dtype)) return LA_EDTYPE;
+    if (n == 0) return LA_OK;
+    if (!p || !g || !m || !v) return LA_EINVAL;
+
+    const uintptr_t addr[5] = {reinterpret_cast<uintptr_t>(p), reinterpret_cast<uintptr_t>(g),
+                               reinterpret_cast<uintptr_t>(m), reinterpret_cast<uintptr_t>(v),
+                               reinterpret_cast<uintptr_t>(p_bf16_out)};
+    const int bytes[5] = {elem_bytes(p_dtype), elem_bytes(g_dtype), elem_bytes(s_dtype), elem_bytes(s_dtype), 2};
+    const int count = p_bf16_out ? 5 : 4;
+    for (int i = 0; i < count; ++i)
+        if (addr[i] % static_cast<uintptr_t>(bytes[i]) != 0) return LA_EINVAL;
+    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
+
+    StepArgs a;
+    a.p = p;
+    a.g = g;
+    a.m = m;
+    a.v = v;
+    a.out = p_bf16_out;
+    a.coef = clip_coef;
+    a.n = n;
+    a.tail_start = n - n % 16;
+    const int h = common_head(addr, bytes, count);
+    if (h < 0 || static_cast<uint64_t>(h) >= a.tail_start) {
+        a.head = 0;
+        a.nvec = 0;
+    } else {
+        a.head = static_cast<uint64_t>(h);
+        a.nvec = (a.tail_start - a.head) / kVec;
+    }
+    a.k.b1 = sc->beta1;
+    a.k.b2 = sc->beta2;
+    a.k.omb1 = sc->one_minus_beta1;
+    a.k.omb2 = sc->one_minus_beta2;
+    a.k.bc2 = sc->bias_correction2;
+    a.k.eps = sc->eps;
+    a.k.step_size = sc->step_size;
+    a.k.w_decay = sc->w_decay;
+    a.k.wd = sc->weight_decay;
+    a.k.mode = sc->decay_mode;
+
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (p_dtype) {
+    case LA_F32: return dispatch_g<float>(g_dtype, s_dtype, a, st);
+    case LA_BF16: return dispatch_g<bf16_t>(g_dtype, s_dtype, a, st);
+    default: return dispatch_g<f16_t>(g_dtype, s_dtype, a, st);
+    }
+}
+
+int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                   int bias_correction, int p_dtype, void* p, int g_dtype, const void* g, int s_dtype, void* m,
+                   void* v, uint64_t n, uint16_t* p_bf16_out, const float* clip_coef, la_stream_t stream)
+{
+    // ds_adam_step checks the dtype triple only after IncrementStep/update_state
+    // (cpu_adam_impl.cpp:241-261), so the state machine advances either way.
+    la_scalars_t sc;
+    int rc = la_scalars(id, step, lr, beta1, beta2, eps, weight_decay, bias_correction, &sc);
+    if (rc != LA_OK) return rc;
+    return la_adamw_step(&sc, p_dtype, p, g_dtype, g, s_dtype, m, v, n, p_bf16_out, clip_coef, stream);
+}
+
+uint64_t la_grad_sqnorm_workspace(uint64_t n) { return static_cast<uint64_t>(norm_grid(n)) * sizeof(double); }
+
+int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, double* partials, uint64_t partials_bytes,
+                   double* sqnorm, int accumulate, la_stream_t stream)
+{
+    if (!dt_valid(g_dtype)) return LA_EDTYPE;
+    if (!sqnorm || !partials) return LA_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(sqnorm) & 7u) || (reinterpret_cast<uintptr_t>(partials) & 7u)) return LA_EINVAL;
+    if (n > 0 && !g) return LA_EINVAL;
+    const int gb = elem_bytes(g_dtype);
+    if (reinterpret_cast<uintptr_t>(g) % static_cast<uintptr_t>(gb)) return LA_EINVAL;
+    const uint32_t grid = norm_grid(n);
+    if (partials_bytes < static_cast<uint64_t>(grid) * sizeof(double)) return LA_EINVAL;
+
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(g);
+    const int h = common_head(&addr, &gb, 1);
+    uint64_t head = 0, nvec = 0;
+    if (h >= 0 && static_cast<uint64_t>(h) < n) {
+        head = static_cast<uint64_t>(h);
+        nvec = (n - head) / kVec;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (g_dtype) {
+    case LA_F32:
+        hipLaunchKernelGGL(la_sqnorm_stage1<float>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
+        break;
+    case LA_BF16:
+        hipLaunchKernelGGL(la_sqnorm_stage1<bf16_t>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
+        break;
+    default:
+        hipLaunchKernelGGL(la_sqnorm_stage1<f16_t>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
+        break;
+    }
+    int rc = hip_rc(hipGetLastError());
+    if (rc != LA_OK) return rc;
+    hipLaunchKernelGGL(la_sqnorm_stage2, dim3(1), dim3(LA_BLOCK), 0, st, partials, grid, sqnorm, accumulate);
+    return hip_rc(hipGetLastError());
+}
+
+int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out, la_stream_t stream)
+{
+    if (!sqnorm || !coef) return LA_EINVAL;
+    hipLaunchKernelGGL(la_clip_coef_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), sqnorm,
+                       max_norm, coef, norm_out);
+    return hip_rc(hipGetLastError());
+}
+
+}  // extern "C"

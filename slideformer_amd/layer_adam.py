@@ -1,0 +1,522 @@
+"""``LayerAdam`` for MI355X: the reference's layer-wise Adam API over a HIP kernel.
+
+Drop-in for ``optimizer/layer_adam/layer_adam.py`` (class ``LayerAdam``,
+layer_adam.py:12-484): same constructor hyper-parameters, the same
+``param_groups`` / ``state`` / ``exp_avg_flat`` / ``exp_avg_sq_flat`` layout and
+the same methods (``add_layer_params``, ``step``, ``step_with_grad_views``,
+``begin_chunk_step`` / ``step_chunk`` / ``end_chunk_step``,
+``update_learning_rate``).  The element update runs in the gfx950 kernel of
+``libslideformer_amd.so`` (C-ABI ``include/layer_adam.h``); the
+beta-power state machine of the reference runs on the host inside that library.
+
+Device tensors are updated in place, asynchronously on the current HIP stream.
+Host tensors (the reference's layout: fp32 master in CPU RAM) are staged
+through HBM in 16 Mi-element pieces and the call returns after completion, as
+the reference's CPU call does.  There is no CPU arithmetic path.
+
+Additions, all keyword-only so that positional signatures are unchanged:
+``bf16_out=`` (the bf16 compute copy written in the same pass), ``clip_coef=``
+(a device fp32 scalar that scales the grads), ``stream=``; and
+``clip_grad_norm(grads, max_norm)`` which produces that coefficient on device.
+"""
+from __future__ import annotations
+
+import ctypes
+import glob
+import itertools
+import math
+import os
+import threading
+from collections import OrderedDict, defaultdict
+from typing import Any, DefaultDict, Dict, Iterable, Optional, Sequence
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.LA_F32, torch.bfloat16: _lib.LA_BF16, torch.float16: _lib.LA_F16}
+_DTYPE_NAME = {torch.float32: "Float", torch.bfloat16: "BFloat16", torch.float16: "Half"}
+
+# the (param, grad, state) triples the reference registers, cpu_adam_impl.cpp:181-189
+SUPPORTED_TRIPLES = frozenset({
+    (torch.float16, torch.float16, torch.float32),
+    (torch.float16, torch.float32, torch.float32),
+    (torch.float16, torch.float16, torch.float16),
+    (torch.bfloat16, torch.bfloat16, torch.float32),
+    (torch.bfloat16, torch.float32, torch.float32),
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16),
+    (torch.float32, torch.float32, torch.float32),
+    (torch.float32, torch.bfloat16, torch.float32),
+    (torch.float32, torch.float16, torch.float32),
+})
+
+# Host tensors are staged through HBM in pieces of this many elements.  A
+# multiple of 16, so that only the last piece of a call holds the reference's
+# scalar tail (the last n % 16 elements of the call).
+HOST_STAGE_ELEMS = 16 * 1024 * 1024
+
+_ids = itertools.count()
+_ids_lock = threading.Lock()
+
+
+def _next_id() -> int:
+    with _ids_lock:
+        return next(_ids)
+
+
+def _stream_handle(stream, device) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _unsupported(p, g, s) -> RuntimeError:
+    # message format of cpu_adam_impl.cpp:256-260
+    return RuntimeError(
+        f"Adam optimizer with param type {_DTYPE_NAME.get(p, p)}, grads type {_DTYPE_NAME.get(g, g)} "
+        f"and state type {_DTYPE_NAME.get(s, s)} is not supported on current hardware")
+
+
+class _ClipWorkspace:
+    """Per-device scratch for the grad-norm reduction (owned here, not by the library)."""
+
+    def __init__(self, device):
+        self.device = device
+        self.partials = torch.empty(0, dtype=torch.float64, device=device)
+        self.sqnorm = torch.zeros(1, dtype=torch.float64, device=device)
+
+    def ensure(self, nbytes: int) -> torch.Tensor:
+        need = max(1, (nbytes + 7) // 8)
+        if self.partials.numel() < need:
+            self.partials = torch.empty(need, dtype=torch.float64, device=self.device)
+        return self.partials
+
+
+class LayerAdam:
+    """Layer-wise Adam/AdamW whose element update runs on the MI355X.
+
+    Mirrors ``LayerAdam`` of the reference (layer_adam.py:12-106): one optimizer
+    instance for all layers; each layer can be stepped on its own.
+    """
+
+    def __init__(
+            self,
+            lr=1e-3,
+            bias_correction=True,
+            betas=(0.9, 0.999),
+            eps=1e-8,
+            weight_decay=0,
+            adamw_mode=True,
+            fp32_optimizer_state=True,
+            num_layer: int = 0,
+            nvme_offload_fraction: float = 0.0,
+            offload_dir: str = '/NVME1',
+            prefetch: bool = True,
+            *,
+            device: Optional[torch.device] = None,
+    ):
+        self.defaults = dict(
+            lr=lr,
+            bias_correction=bias_correction,
+            betas=betas,
+            eps=eps,
+            weight_decay=weight_decay,
+            adamw_mode=adamw_mode,
+        )
+        self.param_groups = []
+
+        # The reference loads its CPU extension here (layer_adam.py:59); this
+        # loads the HIP library and fails loudly if it is missing.
+        self.lib = _lib.load()
+        # The reference always uses id 0 (layer_adam.py:62), so a second
+        # instance would reset the first one's beta-power state; each instance
+        # here gets its own id, and a single instance behaves identically.
+        self.optimizer_id = _next_id()
+        _lib.check(self.lib.la_create(self.optimizer_id, lr, betas[0], betas[1], eps, weight_decay,
+                                      int(bool(adamw_mode)), 0), "la_create")
+
+        self.fp32_optimizer_state = fp32_optimizer_state
+        self.num_layer = num_layer
+        self.device = torch.device(device) if device is not None else None
+        self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
+
+        assert 0.0 <= nvme_offload_fraction <= 1.0
+        self.nvme_offload_fraction = nvme_offload_fraction
+        self.prefetch = prefetch
+        self.pin_memory = nvme_offload_fraction > 0.0
+
+        self.exp_avg_flat = OrderedDict()
+        self.exp_avg_sq_flat = OrderedDict()
+        self._clip_ws: Dict[Any, _ClipWorkspace] = {}
+
+        if self.nvme_offload_fraction > 0.0:
+            # layer_adam.py:92-101; the NVMe state offload is not part of this build.
+            try:
+                from tensornvme import DiskOffloader
+            except ModuleNotFoundError:
+                raise ModuleNotFoundError("Please install tensornvme to use NVMeOptimizer")
+            assert offload_dir is not None, "offload_dir cannot be None"
+            self.offload_dir = offload_dir
+            self.offloader = DiskOffloader(self.offload_dir, 16, 'uring')
+            self.offload_numel = OrderedDict()
+        else:
+            self.offload_dir = None
+            self.offloader = None
+
+    def __del__(self):
+        if hasattr(self, 'lib') and hasattr(self, 'optimizer_id'):
+            try:
+                self.lib.la_destroy(self.optimizer_id)
+            except Exception:
+                pass
+        if getattr(self, 'offloader', None) is not None:
+            del self.offloader
+            if self.offload_dir and os.path.exists(self.offload_dir):
+                try:
+                    for file in glob.glob(os.path.join(self.offload_dir, "offload-*")):
+                        os.remove(file)
+                except OSError:
+                    pass
+
+    # ------------------------------------------------------------------
+    # layer registration (layer_adam.py:127-198)
+    # ------------------------------------------------------------------
+    def _get_layer_numel(self, layer_idx: int) -> int:
+        return sum(p.numel() for p in self.param_groups[layer_idx]['params'])
+
+    def add_layer_params(self, layer_idx: int, params: Iterable[torch.nn.Parameter]) -> int:
+        """Register one layer; allocate its flat m/v beside the params (layer_adam.py:134-198)."""
+        params = list(params)
+        if not params:
+            return -1
+        param_group = {
+            'params': params,
+            'layer_idx': layer_idx,
+            'step': 0,
+            **self.defaults,
+        }
+        self.param_groups.append(param_group)
+        layer_numel = sum(p.numel() for p in params)
+        state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
+        device = params[0].device
+        self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
+        self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
+        offset = 0
+        for p in params:
+            size = p.numel()
+            shape = p.shape
+            if p not in self.state:
+                self.state[p] = {}
+            self.state[p]['exp_avg'] = self.exp_avg_flat[layer_idx][offset:offset + size].view(shape)
+            self.state[p]['exp_avg_sq'] = self.exp_avg_sq_flat[layer_idx][offset:offset + size].view(shape)
+            offset += size
+        if self.offloader is not None:
+            if layer_idx != self.num_layer - 1:
+                self._offload_layer(layer_idx)
+            else:
+                self.offloader.sync_write_events()
+        return layer_idx
+
+    # NVMe hooks, layer_adam.py:200-247 (no-ops without an offloader)
+    def _load_layer(self, layer_idx: int):
+        if self.offloader is None:
+            return
+        if layer_idx < 0:
+            layer_idx = self.num_layer + layer_idx
+        assert layer_idx in self.exp_avg_flat
+        self.offloader.async_read(self.exp_avg_flat[layer_idx])
+        if self.nvme_offload_fraction > 0.5:
+            self.offloader.async_read(self.exp_avg_sq_flat[layer_idx])
+
+    def _offload_layer(self, layer_idx: int):
+        if self.offloader is None:
+            return
+        assert layer_idx in self.exp_avg_flat
+        self.offloader.async_write(self.exp_avg_flat[layer_idx])
+        if self.nvme_offload_fraction > 0.5:
+            self.offloader.async_write(self.exp_avg_sq_flat[layer_idx])
+
+    def _pre_step(self, layer_idx: int):
+        if self.offloader is None:
+            return
+        if self.prefetch:
+            self.offloader.sync_read_events()
+            self._load_layer(layer_idx - 1)
+        else:
+            self._load_layer(layer_idx)
+
+    def _post_step(self, layer_idx: int):
+        if self.offloader is None:
+            return
+        if self.prefetch:
+            self.offloader.sync_write_events()
+        self._offload_layer(layer_idx)
+
+    def torch_adam_update(self, data, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps,
+                          weight_decay, bias_correction1, bias_correction2):
+        """The reference's unused pure-torch formula (layer_adam.py:250-268), kept for API parity."""
+        grad = grad.to(data.dtype)
+        if weight_decay != 0:
+            if self.defaults['adamw_mode']:
+                data.mul_(1 - lr * weight_decay)
+            else:
+                grad = grad.add(data, alpha=weight_decay)
+        exp_avg.mul_(beta1).add_(grad, alpha=1 - beta1)
+        exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)
+        denom = (exp_avg_sq.sqrt() / math.sqrt(bias_correction2)).add_(eps)
+        step_size = lr / bias_correction1
+        data.addcdiv_(exp_avg, denom, value=-step_size)
+
+    # ------------------------------------------------------------------
+    # the native call (cpu_adam.adam_update -> la_adam_update)
+    # ------------------------------------------------------------------
+    def adam_update(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction,
+                    params, grads, exp_avg, exp_avg_sq, *, bf16_out=None, clip_coef=None,
+                    stream=None):
+        """One reference ``adam_update`` call (cpu_adam_impl.cpp:220-270) on the MI355X."""
+        # contiguity checks of cpu_adam_impl.cpp:234-237
+        if not params.is_contiguous():
+            raise RuntimeError("params must be contiguous")
+        if not grads.is_contiguous():
+            raise RuntimeError("grads must be contiguous")
+        if not exp_avg.is_contiguous():
+            raise RuntimeError("exp_avg must be contiguous")
+        if not exp_avg_sq.is_contiguous():
+            raise RuntimeError("exp_avg_sq must be contiguous")
+        n = params.numel()
+        if grads.numel() != n or exp_avg.numel() != n or exp_avg_sq.numel() != n:
+            raise RuntimeError(
+                f"size mismatch: params {n}, grads {grads.numel()}, exp_avg {exp_avg.numel()}, "
+                f"exp_avg_sq {exp_avg_sq.numel()}")
+        if exp_avg_sq.dtype != exp_avg.dtype:
+            raise RuntimeError("exp_avg and exp_avg_sq must have the same dtype")
+        if bf16_out is not None:
+            if bf16_out.dtype != torch.bfloat16 or bf16_out.numel() != n or not bf16_out.is_contiguous():
+                raise RuntimeError("bf16_out must be a contiguous bfloat16 tensor of params.numel() elements")
+        if clip_coef is not None:
+            if clip_coef.dtype != torch.float32 or clip_coef.numel() < 1 or clip_coef.device.type != 'cuda':
+                raise RuntimeError("clip_coef must be a float32 device tensor")
+
+        devs = {t.device for t in (params, grads, exp_avg, exp_avg_sq) if t is not None}
+        if bf16_out is not None:
+            devs.add(bf16_out.device)
+        if len(devs) != 1:
+            raise RuntimeError(f"params/grads/states must be on one device, got {sorted(map(str, devs))}")
+        device = devs.pop()
+        if device.type == 'cuda':
+            self._device_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
+                                grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n)
+        elif device.type == 'cpu':
+            self._host_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
+                              grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n)
+        else:
+            raise RuntimeError(f"unsupported device type: {device.type}")
+
+    def _codes(self, params, grads, exp_avg):
+        key = (params.dtype, grads.dtype, exp_avg.dtype)
+        if key not in SUPPORTED_TRIPLES:
+            raise _unsupported(*key)
+        return _DTYPE_CODE[params.dtype], _DTYPE_CODE[grads.dtype], _DTYPE_CODE[exp_avg.dtype]
+
+    def _scalars(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction):
+        sc = _lib.LaScalars()
+        _lib.check(self.lib.la_scalars(self.optimizer_id, int(step), lr, beta1, beta2, eps,
+                                       weight_decay, int(bool(bias_correction)), ctypes.byref(sc)),
+                   "la_scalars")
+        return sc
+
+    def _device_update(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
+                       grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n):
+        try:
+            pc, gc, sc_ = self._codes(params, grads, exp_avg)
+        except RuntimeError:
+            # the reference advances the state machine before the dtype lookup
+            self._scalars(step, lr, beta1, beta2, eps, weight_decay, bias_correction)
+            raise
+        with torch.cuda.device(params.device):
+            rc = self.lib.la_adam_update(
+                self.optimizer_id, int(step), lr, beta1, beta2, eps, weight_decay,
+                int(bool(bias_correction)), pc, _ptr(params), gc, _ptr(grads), sc_, _ptr(exp_avg),
+                _ptr(exp_avg_sq), n, _ptr(bf16_out), _ptr(clip_coef),
+                _stream_handle(stream, params.device))
+        _lib.check(rc, "la_adam_update")
+
+    def _host_update(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
+                     grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n):
+        """Host tensors: stage through HBM, update there, copy back; returns after completion."""
+        if not torch.cuda.is_available():
+            raise RuntimeError("LayerAdam needs a HIP device (MI355X); there is no CPU arithmetic path")
+        sc = self._scalars(step, lr, beta1, beta2, eps, weight_decay, bias_correction)
+        pc, gc, sc_ = self._codes(params, grads, exp_avg)
+        if n == 0:
+            return
+        device = self.device or torch.device('cuda', torch.cuda.current_device())
+        with torch.cuda.device(device):
+            st = torch.cuda.current_stream(device) if stream is None else stream
+            handle = _stream_handle(st, device)
+            piece = min(n, HOST_STAGE_ELEMS)
+            dp = torch.empty(piece, dtype=params.dtype, device=device)
+            dg = torch.empty(piece, dtype=grads.dtype, device=device)
+            dm = torch.empty(piece, dtype=exp_avg.dtype, device=device)
+            dv = torch.empty(piece, dtype=exp_avg_sq.dtype, device=device)
+            db = torch.empty(piece, dtype=torch.bfloat16, device=device) if bf16_out is not None else None
+            cc = clip_coef.to(device) if clip_coef is not None else None
+            with torch.cuda.stream(st):
+                for cs in range(0, n, piece):
+                    ce = min(cs + piece, n)
+                    k = ce - cs
+                    dp[:k].copy_(params.view(-1)[cs:ce])
+                    dg[:k].copy_(grads.view(-1)[cs:ce])
+                    dm[:k].copy_(exp_avg.view(-1)[cs:ce])
+                    dv[:k].copy_(exp_avg_sq.view(-1)[cs:ce])
+                    rc = self.lib.la_adamw_step(
+                        ctypes.byref(sc), pc, _ptr(dp), gc, _ptr(dg), sc_, _ptr(dm), _ptr(dv), k,
+                        _ptr(db), _ptr(cc), handle)
+                    _lib.check(rc, "la_adamw_step")
+                    params.view(-1)[cs:ce].copy_(dp[:k])
+                    exp_avg.view(-1)[cs:ce].copy_(dm[:k])
+                    exp_avg_sq.view(-1)[cs:ce].copy_(dv[:k])
+                    if bf16_out is not None:
+                        bf16_out.view(-1)[cs:ce].copy_(db[:k])
+            st.synchronize()
+
+    # ------------------------------------------------------------------
+    # steps (layer_adam.py:270-468)
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def step(self, layer_idx: int = None, closure=None):
+        """Update one layer (or all layers) from ``p.grad`` (layer_adam.py:271-359)."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        if layer_idx is not None:
+            groups = [self.param_groups[layer_idx]]
+        else:
+            assert self.offloader is None, "with NVMe offload, layers can only be stepped one at a time, in order"
+            groups = self.param_groups
+        self._pre_step(layer_idx)
+        for param_group in groups:
+            beta1, beta2 = param_group['betas']
+            param_group['step'] += 1
+            for p in param_group['params']:
+                if p.grad is None:
+                    continue
+                state = self.state[p]
+                assert p.data.numel() == p.grad.data.numel(), "params and grads must have the same size"
+                self.adam_update(param_group['step'], param_group['lr'], beta1, beta2,
+                                 param_group['eps'], param_group['weight_decay'],
+                                 param_group['bias_correction'], p.data, p.grad.data,
+                                 state['exp_avg'], state['exp_avg_sq'])
+        self._post_step(layer_idx)
+        return loss
+
+    @torch.no_grad()
+    def step_with_grad_views(self, layer_idx: int = None,
+                             grad_views: Dict[torch.nn.Parameter, torch.Tensor] = None, closure=None):
+        """Like ``step`` but with grads from a ``{param: grad_view}`` dict (layer_adam.py:362-428)."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        if layer_idx is not None:
+            groups = [self.param_groups[layer_idx]]
+        else:
+            assert self.offloader is None, "with NVMe offload, layers can only be stepped one at a time, in order"
+            groups = self.param_groups
+        self._pre_step(layer_idx)
+        for param_group in groups:
+            beta1, beta2 = param_group['betas']
+            param_group['step'] += 1
+            for p in param_group['params']:
+                grad = grad_views.get(p) if grad_views else None
+                if grad is None:
+                    print(f"Warning: no grad view for parameter {p}, skipping update")
+                    continue
+                state = self.state[p]
+                assert p.data.numel() == grad.numel(), "params and grads must have the same size"
+                self.adam_update(param_group['step'], param_group['lr'], beta1, beta2,
+                                 param_group['eps'], param_group['weight_decay'],
+                                 param_group['bias_correction'], p.data, grad,
+                                 state['exp_avg'], state['exp_avg_sq'])
+        self._post_step(layer_idx)
+        return loss
+
+    @torch.no_grad()
+    def begin_chunk_step(self, layer_idx: int):
+        """Start a chunked step: step += 1, NVMe prefetch (layer_adam.py:431-439)."""
+        param_group = self.param_groups[layer_idx]
+        param_group['step'] += 1
+        self._pre_step(layer_idx)
+        return param_group
+
+    @torch.no_grad()
+    def step_chunk(self, param_flat, grad_flat, exp_avg_flat, exp_avg_sq_flat, param_group, *,
+                   bf16_out=None, clip_coef=None, stream=None):
+        """Update one [cs:ce] chunk of flat tensors (layer_adam.py:442-461).
+
+        ``bf16_out``: optional bf16 tensor receiving the compute copy of the
+        updated params.  ``clip_coef``: optional device fp32 scalar multiplying
+        the grads (see ``clip_grad_norm``).  Device tensors: asynchronous on
+        ``stream`` (default: current stream).  Host tensors: returns after completion.
+        """
+        self.adam_update(param_group['step'], param_group['lr'], param_group['betas'][0],
+                         param_group['betas'][1], param_group['eps'], param_group['weight_decay'],
+                         param_group['bias_correction'], param_flat, grad_flat, exp_avg_flat,
+                         exp_avg_sq_flat, bf16_out=bf16_out, clip_coef=clip_coef, stream=stream)
+
+    @torch.no_grad()
+    def end_chunk_step(self, layer_idx: int):
+        """End a chunked step: NVMe write-back (layer_adam.py:464-468)."""
+        self._post_step(layer_idx)
+
+    def update_learning_rate(self, new_lr):
+        """Set ``lr`` in the defaults and every param group (layer_adam.py:470-484)."""
+        self.defaults['lr'] = new_lr
+        for param_group in self.param_groups:
+            param_group['lr'] = new_lr
+
+    # ------------------------------------------------------------------
+    # grad-norm clip (new; the reference has no clipping)
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def clip_grad_norm(self, grads: Sequence[torch.Tensor], max_norm: float, *, stream=None):
+        """Global L2 norm of device grads and the clip coefficient, both on device.
+
+        Returns ``(coef, norm)``: fp32 device scalars with
+        ``coef = min(1, max_norm / (norm + 1e-6))`` (torch.nn.utils.clip_grad_norm_
+        convention).  Pass ``coef`` as ``clip_coef=`` to ``step_chunk``.
+        Nothing is synchronised with the host.
+        """
+        grads = [g for g in grads if g is not None]
+        if not grads:
+            raise RuntimeError("clip_grad_norm needs at least one grad tensor")
+        device = grads[0].device
+        if device.type != 'cuda':
+            raise RuntimeError("clip_grad_norm works on device tensors")
+        ws = self._clip_ws.get(device)
+        if ws is None:
+            ws = self._clip_ws[device] = _ClipWorkspace(device)
+        with torch.cuda.device(device):
+            handle = _stream_handle(stream, device)
+            coef = torch.empty(1, dtype=torch.float32, device=device)
+            norm = torch.empty(1, dtype=torch.float32, device=device)
+            for i, g in enumerate(grads):
+                if g.device != device:
+                    raise RuntimeError("all grads must be on one device")
+                if not g.is_contiguous():
+                    raise RuntimeError("grads must be contiguous")
+                if g.dtype not in _DTYPE_CODE:
+                    raise RuntimeError(f"unsupported grad dtype {g.dtype}")
+                nbytes = self.lib.la_grad_sqnorm_workspace(g.numel())
+                part = ws.ensure(nbytes)
+                _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(part),
+                                                   part.numel() * 8, _ptr(ws.sqnorm), int(i > 0), handle),
+                           "la_grad_sqnorm")
+            _lib.check(self.lib.la_clip_coef(_ptr(ws.sqnorm), float(max_norm), _ptr(coef), _ptr(norm),
+                                             handle), "la_clip_coef")
+        return coef, norm

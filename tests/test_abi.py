@@ -1,0 +1,120 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol,
+and its host-side logic (the beta-power state machine, argument validation,
+workspace sizing) is right.  No kernel is launched here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from slideformer_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "layer_adam.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|uint64_t|const char\*)\s+(la_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert L.la_abi_version() == 1
+
+
+def test_library_is_gfx950_code_object():
+    # the fat binary embeds an amdgcn code object for gfx950 only
+    blob = open(_lib.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in blob
+
+
+def _scalars(L, id_, *args):
+    sc = _lib.LaScalars()
+    assert L.la_scalars(id_, *args, ctypes.byref(sc)) == 0
+    return sc
+
+
+@pytest.mark.parametrize("betas", [(0.9, 0.999), (0.8, 0.95)])
+def test_host_state_machine_matches_oracle(betas):
+    """la_scalars replays IncrementStep/update_state (cpu_adam.h:57-89) bit for bit:
+    multiply path, pow path (several calls per step), step jumps, beta changes,
+    bias_correction off, lr/wd changes."""
+    L = _lib.load()
+    b1, b2 = betas
+    L.la_create(901, 1e-3, b1, b2, 1e-8, 0.01, 1, 0)
+    orc = O.OracleAdam(1e-3, betas, 1e-8, 0.01, True)
+    seq = []
+    for st in range(1, 120):
+        seq.append((st, 1e-3, b1, b2, 1e-8, 0.01, 1))
+        if st % 7 == 0:
+            seq.append((st, 1e-3, b1, b2, 1e-8, 0.01, 1))          # second chunk: pow path
+    seq += [(500, 2e-4, b1, b2, 1e-6, 0.1, 1), (501, 2e-4, b1, b2, 1e-6, 0.1, 0),
+            (502, 2e-4, 0.85, b2, 1e-6, 0.1, 1), (503, 2e-4, 0.85, b2, 1e-6, 0.0, 1),
+            (1, 1e-3, b1, b2, 1e-8, 0.01, 1)]
+    lib = O.lib()
+    for (st, lr, bb1, bb2, eps, wd, bc) in seq:
+        sc = _scalars(L, 901, st, lr, bb1, bb2, eps, wd, bc)
+        lib.orc_increment_step(orc.s, st, bb1, bb2)
+        lib.orc_update_state(orc.s, lr, eps, wd, bc)
+        ref = orc.scalars()  # b1t, b2t, bc1, bc2, step_size, w_decay, 1-b1, 1-b2
+        got = np.array([sc.beta1_t, sc.beta2_t, sc.bias_correction1, sc.bias_correction2,
+                        sc.step_size, sc.w_decay, sc.one_minus_beta1, sc.one_minus_beta2],
+                       dtype=np.float32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (st, got, ref)
+        assert sc.step == orc.s.step
+        assert sc.decay_mode == (0 if np.float32(wd) <= 0 else 2)
+    L.la_destroy(901)
+
+
+def test_l2_mode_flag():
+    L = _lib.load()
+    L.la_create(902, 1e-3, 0.9, 0.999, 1e-8, 0.1, 0, 0)
+    sc = _scalars(L, 902, 1, 1e-3, 0.9, 0.999, 1e-8, 0.1, 1)
+    assert sc.decay_mode == 1 and sc.weight_decay == np.float32(0.1)
+    L.la_destroy(902)
+
+
+def test_error_codes_without_launch():
+    L = _lib.load()
+    sc = _lib.LaScalars()
+    # unknown id
+    assert L.la_scalars(123456, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.byref(sc)) == _lib.LA_EINVAL
+    assert L.la_adam_update(123456, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0, None, 1, None, 0, None, None,
+                            10, None, None, None) == _lib.LA_EINVAL
+    # unregistered dtype triples (cpu_adam_impl.cpp:181-189) and unknown codes
+    for trip in [(0, 0, 1), (1, 2, 0), (2, 1, 0), (1, 1, 2), (0, 1, 2), (7, 0, 0)]:
+        assert L.la_adamw_step(ctypes.byref(sc), trip[0], None, trip[1], None, trip[2], None, None, 10,
+                               None, None, None) == _lib.LA_EDTYPE
+    # n == 0 is a no-op (the reference test registers an empty layer)
+    assert L.la_adamw_step(ctypes.byref(sc), 0, None, 1, None, 0, None, None, 0, None, None, None) == 0
+    # null buffers with n > 0
+    assert L.la_adamw_step(ctypes.byref(sc), 0, None, 1, None, 0, None, None, 5, None, None, None) == _lib.LA_EINVAL
+    # misaligned element pointers (odd address for a 4-byte type)
+    assert L.la_adamw_step(ctypes.byref(sc), 0, 0x1001, 1, 0x2000, 0, 0x3000, 0x4000, 5, None, None,
+                           None) == _lib.LA_EINVAL
+    assert L.la_grad_sqnorm(1, None, 10, None, 0, None, 0, None) == _lib.LA_EINVAL
+    assert L.la_clip_coef(None, 1.0, None, None, None) == _lib.LA_EINVAL
+    assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
+
+
+def test_grad_sqnorm_workspace_is_bounded():
+    L = _lib.load()
+    assert L.la_grad_sqnorm_workspace(0) == 8
+    assert L.la_grad_sqnorm_workspace(1) == 8
+    assert L.la_grad_sqnorm_workspace(8 * 256 * 3) == 3 * 8
+    # bounded by the stage-1 grid cap, so stage 2 is one workgroup
+    assert L.la_grad_sqnorm_workspace(1 << 40) == L.la_grad_sqnorm_workspace(1 << 35)
+    assert L.la_grad_sqnorm_workspace(1 << 40) <= 64 * 1024

@@ -1,0 +1,147 @@
+"""The LayerAdam API (drop-in for optimizer/layer_adam/layer_adam.py) on the MI355X."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from slideformer_amd import LayerAdam
+from tests import _hip as H
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_known_answer_vs_torch_adamw(gdtype, hip_device):
+    """The reference's only numeric test, test_shared_data_parallel.py:53-93, single
+    process: sizes (19, 3, 0) in chunks of 5, five steps, lr change at step 3."""
+    adam = LayerAdam(lr=0.01, betas=(0.8, 0.95), eps=1e-6, weight_decay=0.1)
+    chunk = 5
+    for layer, size in enumerate((19, 3, 0)):
+        initial = torch.linspace(-0.5, 0.5, size)
+        params = initial.clone().to(hip_device)
+        first = torch.zeros(size, device=hip_device)
+        second = torch.zeros(size, device=hip_device)
+        reference = torch.nn.Parameter(initial.clone())
+        tadam = torch.optim.AdamW([reference], lr=0.01, betas=(0.8, 0.95), eps=1e-6,
+                                  weight_decay=0.1, foreach=False)
+        for step in range(1, 6):
+            grads = ((torch.arange(size) * 0.13 + step * 0.2).sin() * 0.1).to(gdtype)
+            gd = grads.to(hip_device)
+            lr = 0.01 if step < 3 else 0.003
+            tadam.param_groups[0]["lr"] = lr
+            for start in range(0, size, chunk):
+                end = min(start + chunk, size)
+                adam.step_chunk(params[start:end], gd[start:end], first[start:end], second[start:end],
+                                dict(adam.defaults, step=step, lr=lr))
+            reference.grad = grads.float()
+            tadam.step()
+            torch.testing.assert_close(params.cpu(), reference.detach(), rtol=1e-6, atol=1e-7)
+            st = tadam.state[reference]
+            torch.testing.assert_close(first.cpu(), st["exp_avg"])
+            torch.testing.assert_close(second.cpu(), st["exp_avg_sq"])
+
+
+def _oracle_layer_step(orc, step, pieces, grads, ms, vs):
+    for p, g, m, v in zip(pieces, grads, ms, vs):
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, g16="bf16")
+
+
+def test_step_per_tensor_and_grad_views(hip_device):
+    """step(layer_idx) and step_with_grad_views call adam_update once per tensor
+    (layer_adam.py:299-327, 391-422), which matters for the scalar tails."""
+    shapes = [(37, 5), (5,), (64, 3), (1,)]
+    rng = np.random.default_rng(0)
+    init = [rng.normal(0, 0.02, int(np.prod(s))).astype(np.float32) for s in shapes]
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).view(s).to(hip_device)) for x, s in zip(init, shapes)]
+    assert adam.add_layer_params(0, params) == 0
+    assert adam.add_layer_params(1, []) == -1
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    hp = [x.copy() for x in init]
+    hm = [np.zeros_like(x) for x in init]
+    hv = [np.zeros_like(x) for x in init]
+    for step in range(1, 4):
+        grads = [torch.from_numpy(rng.normal(0, 1e-3, x.size).astype(np.float32)).bfloat16() for x in init]
+        gbits = [H.to_np_bits(g, "bf16") for g in grads]
+        if step % 2:
+            for p, g, s in zip(params, grads, shapes):
+                p.grad = g.view(s).to(hip_device)
+            adam.step(0)
+        else:
+            adam.step_with_grad_views(0, {p: g.view(s).to(hip_device) for p, g, s in zip(params, grads, shapes)})
+        _oracle_layer_step(orc, step, hp, gbits, hm, hv)
+    torch.cuda.synchronize()
+    assert adam.param_groups[0]["step"] == 3
+    for p, x, m, v in zip(params, hp, hm, hv):
+        assert np.array_equal(H.to_np_bits(p.data.reshape(-1), "f32"), x.view(np.uint32))
+        st = adam.state[p]
+        assert np.array_equal(H.to_np_bits(st["exp_avg"].reshape(-1), "f32"), m.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(st["exp_avg_sq"].reshape(-1), "f32"), v.view(np.uint32))
+
+
+def test_host_tensors_are_staged_through_hbm(hip_device):
+    """The reference's layout (fp32 master + bf16 grads in host RAM) still works:
+    the update runs on the GPU in 16 Mi-element pieces and the call returns after
+    completion.  Bit-exact with the oracle across a piece boundary."""
+    from slideformer_amd.layer_adam import HOST_STAGE_ELEMS
+    n = HOST_STAGE_ELEMS + 21
+    rng = np.random.default_rng(5)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32))
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    out = torch.empty(n, dtype=torch.bfloat16)
+    ph, mh, vh = p.numpy().copy(), m.numpy().copy(), v.numpy().copy()
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=step), bf16_out=out)
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16")
+    assert np.array_equal(p.numpy().view(np.uint32), ph.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
+    assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16), O.f32_to_bf16(ph))
+
+
+def test_clip_grad_norm_and_side_stream(hip_device):
+    n = 3_000_017
+    rng = np.random.default_rng(8)
+    adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(hip_device)
+    m = torch.zeros(n, device=hip_device)
+    v = torch.zeros(n, device=hip_device)
+    g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16().to(hip_device)
+    ph = p.cpu().numpy().copy()
+    mh = np.zeros(n, np.float32)
+    vh = np.zeros(n, np.float32)
+    side = torch.cuda.Stream(device=hip_device)
+    side.wait_stream(torch.cuda.current_stream(hip_device))
+    with torch.cuda.stream(side):
+        coef, norm = adam.clip_grad_norm([g[:1000], g[1000:]], 1.0, stream=side)
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=1), clip_coef=coef, stream=side)
+    side.synchronize()
+    sq = O.grad_sqnorm(H.to_np_bits(g, "bf16"), "bf16")
+    c_ref, n_ref = O.clip_coef(sq, 1.0)
+    assert coef.item() == np.float32(c_ref) and norm.item() == np.float32(n_ref) and c_ref < 1
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    orc.update(1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16",
+               clip_coef=float(coef.item()))
+    assert np.array_equal(H.to_np_bits(p, "f32"), ph.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(m, "f32"), mh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(v, "f32"), vh.view(np.uint32))
+
+
+def test_errors(hip_device):
+    adam = LayerAdam()
+    a = torch.zeros(10, device=hip_device)
+    with pytest.raises(RuntimeError, match="params must be contiguous"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, torch.zeros(10, 2, device=hip_device).t(),
+                         a, a, a)
+    with pytest.raises(RuntimeError, match="is not supported on current hardware"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a.bfloat16(), a.bfloat16())
+    with pytest.raises(RuntimeError, match="one device"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a.cpu(), a, a)
+    with pytest.raises(RuntimeError, match="size mismatch"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a[:5], a, a)

@@ -1,0 +1,362 @@
+"""Parity of the HIP LayerAdam step (through the C-ABI) with the CPU checker.
+
+Bar: fp32 p/m/v and 16-bit states bit-exact against the oracle (which is
+itself bit-exact against the reference compiled from its sources, see
+test_oracle.py); the bf16 compute copy bit-exact to RNE of the updated fp32
+master; the grad norm within 1e-12 relative of the float64 sequential sum
+(the tolerance north_star allows is 1e-6); NaN compared as a class.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests import _golden as G
+from tests import _hip as H
+
+pytestmark = pytest.mark.gpu
+
+KIND16 = {"bf16": "bf16", "f16": "f16", "f32": None}
+
+
+def _view(bits_arr, kind):
+    return bits_arr.view(np.float32) if kind == "f32" else bits_arr
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures written by the compiled reference
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", G.case_names())
+def test_hip_reproduces_golden(name, hip_device):
+    log(f"golden case {name}")
+    meta, arrays = G.get_case(name)
+    pk, gk, sk = meta["triple"]
+    b1, b2 = meta["betas"]
+    opt = H.HipAdam(1e-3, (b1, b2), meta["eps"], meta["wd"], meta["adamw"])
+    dev = {}
+
+    def call(step, lr, p, g, m, v, lo, hi):
+        # keep the state resident; upload the step's grads once per step
+        if "p" not in dev:
+            dev["p"] = H.to_dev_bits(p, pk, hip_device)
+            dev["m"] = H.to_dev_bits(m, sk, hip_device)
+            dev["v"] = H.to_dev_bits(v, sk, hip_device)
+        if dev.get("gstep") != step:
+            dev["g"] = H.to_dev_bits(g, gk, hip_device)
+            dev["gstep"] = step
+        opt.update(step, lr, b1, b2, meta["eps"], meta["wd"], meta["bc"], dev["p"][lo:hi],
+                   dev["g"][lo:hi], dev["m"][lo:hi], dev["v"][lo:hi])
+        if hi == sum(meta["sizes"]):
+            p[:] = H.to_np_bits(dev["p"], pk)
+            m[:] = H.to_np_bits(dev["m"], sk)
+            v[:] = H.to_np_bits(dev["v"], sk)
+
+    got = G.replay(meta, arrays, call)
+    assert G.mismatches(meta, arrays, got) == (0, 0, 0)
+
+
+# ---------------------------------------------------------------------------
+# config C1: one GPT-2-small block, 10 steps, bf16 copy emitted
+# ---------------------------------------------------------------------------
+
+GPT2_SIZES = [768, 768, 768 * 2304, 2304, 768 * 768, 768, 768, 768, 768 * 3072, 3072, 3072 * 768, 768]
+
+
+def test_c1_gpt2_block_ten_steps(hip_device):
+    from slideformer_amd import LayerAdam
+    n = sum(GPT2_SIZES)
+    assert n == 7_087_872
+    log(f"C1 n={n}")
+    rng = np.random.default_rng(1)
+    p_host = rng.normal(0, 0.02, n).astype(np.float32)
+    m_host = np.zeros(n, np.float32)
+    v_host = np.zeros(n, np.float32)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+
+    opt = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    p_dev = torch.from_numpy(p_host.copy()).to(hip_device)
+    params = [torch.nn.Parameter(t) for t in torch.split(p_dev, GPT2_SIZES)]
+    idx = opt.add_layer_params(0, params)
+    assert idx == 0 and opt.exp_avg_flat[0].device == p_dev.device
+    out = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    for step in range(1, 11):
+        g32 = np.random.default_rng(1000 + step).normal(0, 1e-3, n).astype(np.float32)
+        g_bf = torch.from_numpy(g32).bfloat16()
+        g_bits = H.to_np_bits(g_bf, "bf16")
+        group = opt.begin_chunk_step(0)
+        opt.step_chunk(p_dev, g_bf.to(hip_device), opt.exp_avg_flat[0], opt.exp_avg_sq_flat[0], group,
+                       bf16_out=out)
+        opt.end_chunk_step(0)
+        orc.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p_host, g_bits, m_host, v_host, g16="bf16")
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p_dev, "f32"), p_host.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(opt.exp_avg_flat[0], "f32"), m_host.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(opt.exp_avg_sq_flat[0], "f32"), v_host.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(p_host))
+    # the per-param views see the flat buffer (layer_adam.py:176-189)
+    assert torch.equal(params[2].data, p_dev[1536:1536 + 768 * 2304])
+
+
+# ---------------------------------------------------------------------------
+# tails, misaligned sub-views, every dtype triple
+# ---------------------------------------------------------------------------
+
+SIZES = [1, 3, 7, 8, 15, 16, 17, 31, 63, 64, 127, 129, 1023, 4097, 100_003]
+
+
+@pytest.mark.parametrize("offsets", [(0, 0, 0, 0), (1, 1, 1, 1), (3, 3, 3, 3), (5, 5, 5, 5),
+                                     (0, 1, 0, 0), (2, 0, 4, 6), (7, 3, 1, 0)])
+def test_sizes_and_misaligned_offsets(offsets, hip_device):
+    op, og, om, ov = offsets
+    log(f"offsets {offsets}")
+    rng = np.random.default_rng(sum(offsets) * 31 + op)
+    opt = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    total = sum(SIZES)
+    P = torch.from_numpy(rng.normal(0, 0.02, total + 8).astype(np.float32)).to(hip_device)
+    M = torch.from_numpy(rng.normal(0, 1e-3, total + 8).astype(np.float32)).to(hip_device)
+    V = torch.from_numpy(np.abs(rng.normal(0, 1e-6, total + 8)).astype(np.float32)).to(hip_device)
+    OUT = torch.zeros(total + 8, dtype=torch.bfloat16, device=hip_device)
+    ph, mh, vh = H.to_np_bits(P, "f32"), H.to_np_bits(M, "f32"), H.to_np_bits(V, "f32")
+    for step in (1, 2):
+        gb = torch.from_numpy(rng.normal(0, 1e-3, total + 8).astype(np.float32)).bfloat16()
+        G_ = gb.to(hip_device)
+        gh = H.to_np_bits(gb, "bf16")
+        lo = 0
+        for n in SIZES:
+            opt.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, P[op + lo:op + lo + n],
+                       G_[og + lo:og + lo + n], M[om + lo:om + lo + n], V[ov + lo:ov + lo + n],
+                       out=OUT[op + lo:op + lo + n])
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph.view(np.float32)[op + lo:op + lo + n],
+                       gh[og + lo:og + lo + n], mh.view(np.float32)[om + lo:om + lo + n],
+                       vh.view(np.float32)[ov + lo:ov + lo + n], g16="bf16")
+            lo += n
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(P, "f32"), ph)
+    assert np.array_equal(H.to_np_bits(M, "f32"), mh)
+    assert np.array_equal(H.to_np_bits(V, "f32"), vh)
+    out = H.to_np_bits(OUT, "bf16")
+    seg = slice(op, op + total)
+    assert np.array_equal(out[seg], O.f32_to_bf16(ph.view(np.float32)[seg]))
+
+
+TRIPLES = [("f32", "bf16", "f32"), ("f32", "f32", "f32"), ("f32", "f16", "f32"),
+           ("bf16", "bf16", "f32"), ("bf16", "f32", "f32"), ("bf16", "bf16", "bf16"),
+           ("f16", "f16", "f32"), ("f16", "f32", "f32"), ("f16", "f16", "f16")]
+
+
+@pytest.mark.parametrize("triple", TRIPLES)
+@pytest.mark.parametrize("mode", ["adamw", "l2", "none", "no_bc"])
+def test_every_triple_and_mode(triple, mode, hip_device):
+    pk, gk, sk = triple
+    log(f"triple {triple} mode {mode}")
+    wd = 0.0 if mode == "none" else 0.05
+    adamw = mode != "l2"
+    bc = mode != "no_bc"
+    rng = np.random.default_rng(abs(hash((triple, mode))) % (2**31))
+    sizes = (100_003, 4096, 13)
+    n = sum(sizes)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(H.TD[pk])
+    m = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(H.TD[sk])
+    v = torch.from_numpy(np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)).to(H.TD[sk])
+    ph, mh, vh = H.to_np_bits(p, pk), H.to_np_bits(m, sk), H.to_np_bits(v, sk)
+    pd, md, vd = p.to(hip_device), m.to(hip_device), v.to(hip_device)
+    opt = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, wd, adamw)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, wd, adamw)
+    for step in (1, 2, 3):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(H.TD[gk])
+        gh = H.to_np_bits(g, gk)
+        gd = g.to(hip_device)
+        lo = 0
+        for size in sizes:
+            hi = lo + size
+            opt.update(step, 1e-3, 0.9, 0.999, 1e-8, wd, bc, pd[lo:hi], gd[lo:hi], md[lo:hi], vd[lo:hi])
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, wd, bc, _view(ph, pk)[lo:hi], _view(gh, gk)[lo:hi],
+                       _view(mh, sk)[lo:hi], _view(vh, sk)[lo:hi], p16=KIND16[pk], g16=KIND16[gk],
+                       s16=KIND16[sk])
+            lo = hi
+    torch.cuda.synchronize()
+    assert G.same_bits(H.to_np_bits(pd, pk), ph, pk).all()
+    assert G.same_bits(H.to_np_bits(md, sk), mh, sk).all()
+    assert G.same_bits(H.to_np_bits(vd, sk), vh, sk).all()
+
+
+def test_denormal_and_extreme_values(hip_device):
+    """Subnormal v and grads, zero grads, huge grads: IEEE denormals are kept."""
+    log("denormals")
+    n = 4096 + 5
+    rng = np.random.default_rng(9)
+    g = rng.normal(0, 1e-3, n).astype(np.float32)
+    g[0::3] = rng.normal(0, 1e-22, g[0::3].size)   # squares underflow into subnormals
+    g[1::7] = 0.0
+    g[2::11] = rng.normal(0, 1e3, g[2::11].size)
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    p[5::13] = 1e-40                                # subnormal params
+    m = np.zeros(n, np.float32)
+    v = np.full(n, 1e-44, np.float32)               # subnormal second moment
+    pd, gd, md, vd = (torch.from_numpy(x.copy()).to(hip_device) for x in (p, g, m, v))
+    opt = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        opt.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, pd, gd, md, vd)
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g.copy(), m, v)
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(pd, "f32"), p.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(md, "f32"), m.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(vd, "f32"), v.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# grad norm + clip
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 7, 4097, 1_000_003, 16 * 1024 * 1024 + 5])
+@pytest.mark.parametrize("gk", ["bf16", "f32", "f16"])
+def test_grad_sqnorm(n, gk, hip_device):
+    log(f"sqnorm n={n} {gk}")
+    rng = np.random.default_rng(n)
+    g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(H.TD[gk])
+    gh = H.to_np_bits(g, gk)
+    gd = g.to(hip_device)
+    sq = H.sqnorm(gd)
+    sq2 = H.sqnorm(gd)
+    exact = O.grad_sqnorm(_view(gh, gk), KIND16[gk])
+    got = float(sq.item())
+    assert abs(got - exact) <= 1e-12 * exact
+    assert sq.item() == sq2.item()  # deterministic
+    # odd offset (scalar head) gives the same sum over the same elements
+    if n > 1:
+        sub = gd[1:]
+        exact_sub = O.grad_sqnorm(_view(gh, gk)[1:], KIND16[gk])
+        assert abs(float(H.sqnorm(sub).item()) - exact_sub) <= 1e-12 * exact_sub
+
+
+def test_grad_sqnorm_accumulates_over_buffers(hip_device):
+    rng = np.random.default_rng(2)
+    parts = [torch.from_numpy(rng.normal(0, 1e-3, k).astype(np.float32)).bfloat16() for k in (1000, 3, 77777)]
+    acc = H.sqnorm(parts[0].to(hip_device))
+    for t in parts[1:]:
+        H.sqnorm(t.to(hip_device), accumulate_into=acc)
+    exact = sum(O.grad_sqnorm(H.to_np_bits(t, "bf16"), "bf16") for t in parts)
+    assert abs(acc.item() - exact) <= 1e-12 * exact
+
+
+def test_clip_coef_matches_oracle_and_torch(hip_device):
+    for scale, max_norm in ((1e-3, 1.0), (1e-1, 1.0), (1e-6, 1.0), (1.0, 0.5)):
+        g = torch.from_numpy(np.random.default_rng(4).normal(0, scale, 300001).astype(np.float32))
+        gd = g.to(hip_device)
+        sq = H.sqnorm(gd)
+        coef, norm = H.clip_coef(sq, max_norm)
+        c_ref, n_ref = O.clip_coef(float(sq.item()), max_norm)
+        assert coef.item() == np.float32(c_ref) and norm.item() == np.float32(n_ref)
+        w = torch.nn.Parameter(g.clone())
+        w.grad = g.clone()
+        total = torch.nn.utils.clip_grad_norm_([w], max_norm)
+        assert abs(total.item() - norm.item()) <= 2e-7 * norm.item()
+
+
+def test_clip_non_finite_norm_propagates(hip_device):
+    g = torch.zeros(1000, dtype=torch.bfloat16)
+    g[10] = float("inf")
+    sq = H.sqnorm(g.to(hip_device))
+    coef, norm = H.clip_coef(sq, 1.0)
+    assert np.isinf(norm.item()) and coef.item() == 0.0
+    g[11] = float("nan")
+    sq = H.sqnorm(g.to(hip_device))
+    coef, norm = H.clip_coef(sq, 1.0)
+    assert np.isnan(norm.item()) and np.isnan(coef.item())
+
+
+# ---------------------------------------------------------------------------
+# configs C2 and C4 at full size
+# ---------------------------------------------------------------------------
+
+def llama8b_layer_sizes():
+    h, kv, ffn = 4096, 1024, 14336
+    return [h * h, h * kv, h * kv, h * h, h * ffn, h * ffn, ffn * h, h, h]
+
+
+def qwen14b_layer_sizes():
+    h, kv, ffn = 5120, 1024, 13824
+    return [h * h, h, h * kv, kv, h * kv, kv, h * h, h * ffn, h * ffn, ffn * h, h, h]
+
+
+def _dev_normal(n, std, seed, device, dtype=torch.float32):
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    return (torch.randn(n, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+
+def _full_size_step(n, device, *, warm_steps, wd, seed, outliers=False, max_norm=1.0, chunk=None):
+    """Warm m/v with the oracle, then one clipped step on both sides; compare bits."""
+    log(f"full-size n={n} warm={warm_steps} wd={wd} outliers={outliers}")
+    p_d = _dev_normal(n, 0.02, seed, device)
+    p_h = p_d.cpu().numpy().copy()
+    m_h = np.zeros(n, np.float32)
+    v_h = np.zeros(n, np.float32)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, wd, True)
+    for st in range(1, warm_steps + 1):
+        g = _dev_normal(n, 1e-3, seed + st, device, torch.bfloat16)
+        orc.update(st, 1e-5, 0.9, 0.999, 1e-8, wd, True, p_h, H.to_np_bits(g, "bf16"), m_h, v_h, g16="bf16")
+    st = warm_steps + 1
+    g = _dev_normal(n, 1e-3, seed + st, device, torch.bfloat16)
+    if outliers:
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed + 777)
+        idx = torch.randint(0, n, (n // 1000,), generator=gen, device=device)
+        g[idx] = g[idx] * 100
+    g_h = H.to_np_bits(g, "bf16")
+    p_d = torch.from_numpy(p_h.copy()).to(device)
+    m_d = torch.from_numpy(m_h.copy()).to(device)
+    v_d = torch.from_numpy(v_h.copy()).to(device)
+    out = torch.empty(n, dtype=torch.bfloat16, device=device)
+
+    sq = H.sqnorm(g)
+    coef, norm = H.clip_coef(sq, max_norm)
+    exact = O.grad_sqnorm(g_h, "bf16")
+    assert abs(sq.item() - exact) <= 1e-12 * exact
+    c = float(coef.item())
+    assert c < 1.0  # clipping triggers at this grad scale
+
+    hip = H.HipAdam(1e-5, (0.9, 0.999), 1e-8, wd, True)
+    # replay the warm-up calls on the host state machine (one call per step)
+    for s in range(1, warm_steps + 1):
+        sc = H._lib.LaScalars()
+        H._lib.check(hip.L.la_scalars(hip.id, s, 1e-5, 0.9, 0.999, 1e-8, wd, 1, H.ctypes.byref(sc)), "scalars")
+    chunk = chunk or n
+    for lo in range(0, n, chunk):
+        hi = min(lo + chunk, n)
+        hip.update(st, 1e-5, 0.9, 0.999, 1e-8, wd, True, p_d[lo:hi], g[lo:hi], m_d[lo:hi], v_d[lo:hi],
+                   out=out[lo:hi], coef=coef)
+        orc.update(st, 1e-5, 0.9, 0.999, 1e-8, wd, True, p_h[lo:hi], g_h[lo:hi], m_h[lo:hi], v_h[lo:hi],
+                   g16="bf16", clip_coef=c)
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p_d, "f32"), p_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(m_d, "f32"), m_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(v_d, "f32"), v_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(p_h))
+
+
+def test_c2_llama8b_layer_full_size(hip_device):
+    n = sum(llama8b_layer_sizes())
+    assert n == 218_112_000
+    _full_size_step(n, hip_device, warm_steps=5, wd=0.01, seed=20)
+
+
+def test_c2_llama8b_layer_in_reference_chunks(hip_device):
+    """The runtime's chunking: 32 Mi-element step_chunk calls (transformer_layer.py:26-27)."""
+    n = sum(llama8b_layer_sizes())
+    _full_size_step(n, hip_device, warm_steps=1, wd=0.01, seed=40, chunk=32 * 1024 * 1024)
+
+
+def test_c4_qwen14b_layer_outliers(hip_device):
+    n = sum(qwen14b_layer_sizes())
+    assert n == 275_268_608
+    _full_size_step(n, hip_device, warm_steps=0, wd=0.1, seed=30, outliers=True)

@@ -1,0 +1,107 @@
+"""Host-side behaviour of the LayerAdam drop-in (no GPU needed)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from slideformer_amd import LayerAdam, SUPPORTED_TRIPLES
+from slideformer_amd.optimizer import LayerAdam as LayerAdamAlias
+
+
+def test_import_paths():
+    assert LayerAdamAlias is LayerAdam
+
+
+def test_constructor_defaults_match_reference():
+    # layer_adam.py:17-30, 46-53
+    adam = LayerAdam()
+    assert adam.defaults == dict(lr=1e-3, bias_correction=True, betas=(0.9, 0.999), eps=1e-8,
+                                 weight_decay=0, adamw_mode=True)
+    assert adam.param_groups == [] and adam.offloader is None and adam.offload_dir is None
+    assert adam.fp32_optimizer_state is True and adam.num_layer == 0 and adam.pin_memory is False
+
+
+def test_unique_optimizer_ids():
+    assert LayerAdam().optimizer_id != LayerAdam().optimizer_id
+
+
+def test_add_layer_params_layout():
+    adam = LayerAdam(lr=2e-4, weight_decay=0.01)
+    params = [torch.nn.Parameter(torch.randn(3, 4)), torch.nn.Parameter(torch.randn(5))]
+    assert adam.add_layer_params(0, params) == 0
+    assert adam.add_layer_params(1, []) == -1
+    g = adam.param_groups[0]
+    assert g["layer_idx"] == 0 and g["step"] == 0 and g["lr"] == 2e-4 and g["params"] == params
+    assert adam.exp_avg_flat[0].shape == (17,) and adam.exp_avg_flat[0].dtype == torch.float32
+    assert adam.exp_avg_sq_flat[0].abs().sum() == 0
+    st = adam.state[params[0]]
+    assert st["exp_avg"].shape == (3, 4)
+    assert st["exp_avg"].data_ptr() == adam.exp_avg_flat[0].data_ptr()
+    assert adam.state[params[1]]["exp_avg_sq"].data_ptr() == adam.exp_avg_sq_flat[0].data_ptr() + 12 * 4
+
+
+def test_state_dtype_follows_params_when_not_fp32():
+    adam = LayerAdam(fp32_optimizer_state=False)
+    adam.add_layer_params(0, [torch.nn.Parameter(torch.randn(4).bfloat16())])
+    assert adam.exp_avg_flat[0].dtype == torch.bfloat16
+
+
+def test_begin_chunk_step_and_lr_update():
+    adam = LayerAdam()
+    adam.add_layer_params(0, [torch.nn.Parameter(torch.randn(4))])
+    adam.add_layer_params(1, [torch.nn.Parameter(torch.randn(4))])
+    g = adam.begin_chunk_step(1)
+    assert g is adam.param_groups[1] and g["step"] == 1 and adam.param_groups[0]["step"] == 0
+    adam.end_chunk_step(1)
+    adam.update_learning_rate(5e-5)
+    assert adam.defaults["lr"] == 5e-5 and all(pg["lr"] == 5e-5 for pg in adam.param_groups)
+
+
+def test_supported_triples_are_the_references_nine():
+    # cpu_adam_impl.cpp:181-189
+    assert len(SUPPORTED_TRIPLES) == 9
+    assert (torch.float32, torch.bfloat16, torch.float32) in SUPPORTED_TRIPLES
+    assert (torch.float32, torch.float32, torch.bfloat16) not in SUPPORTED_TRIPLES
+
+
+def test_host_tensors_without_gpu_fail_loudly():
+    if torch.cuda.is_available():
+        pytest.skip("a HIP device is present")
+    adam = LayerAdam()
+    p = torch.nn.Parameter(torch.randn(8))
+    adam.add_layer_params(0, [p])
+    p.grad = torch.randn(8)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        adam.step(0)
+
+
+def test_argument_checks_precede_dispatch():
+    adam = LayerAdam()
+    a = torch.zeros(10)
+    with pytest.raises(RuntimeError, match="grads must be contiguous"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, torch.zeros(10, 2).t()[0], a, a)
+    with pytest.raises(RuntimeError, match="size mismatch"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a[:3], a, a)
+    with pytest.raises(RuntimeError, match="bf16_out"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a, a, bf16_out=torch.zeros(10))
+
+
+def test_nvme_offload_needs_tensornvme():
+    try:
+        import tensornvme  # noqa: F401
+        pytest.skip("tensornvme installed")
+    except ModuleNotFoundError:
+        pass
+    with pytest.raises(ModuleNotFoundError, match="tensornvme"):
+        LayerAdam(nvme_offload_fraction=0.5)
+
+
+def test_torch_adam_update_formula():
+    # the reference's unused pure-torch path, layer_adam.py:250-268
+    adam = LayerAdam(weight_decay=0.1)
+    data = torch.ones(4)
+    grad = torch.full((4,), 0.5)
+    m, v = torch.zeros(4), torch.zeros(4)
+    adam.torch_adam_update(data, grad, m, v, 0.1, 0.9, 0.999, 1e-8, 0.1, 1 - 0.9, 1 - 0.999)
+    expected = 1.0 * (1 - 0.1 * 0.1) - 0.1 * 1.0
+    torch.testing.assert_close(data, torch.full((4,), expected), rtol=1e-5, atol=1e-6)
