@@ -266,14 +266,21 @@ int orc_adam_update(orc_adam_t* s, uint64_t step, float lr, float b1, float b2, 
 /* grad norm + clip coefficient                                        */
 /* ------------------------------------------------------------------ */
 
+/* Compensated (Neumaier) float64 sum of the exact squares, so that the result
+ * is the true sum to about one ulp of binary64 whatever the length; any
+ * summation order (the GPU's tree) is then compared against the exact value. */
 double orc_grad_sqnorm(int g_dtype, const void* g, uint64_t n)
 {
-    double acc = 0.0;
+    double s = 0.0, c = 0.0;
     for (uint64_t i = 0; i < n; ++i) {
         double x = (double)load_as_f32(g_dtype, g, i);
-        acc += x * x;  /* x*x is exact in binary64 for any binary32 x */
+        double y = x * x;  /* exact in binary64 for any binary32 x */
+        double t = s + y;
+        if (fabs(s) >= fabs(y)) c += (s - t) + y;
+        else c += (y - t) + s;
+        s = t;
     }
-    return acc;
+    return s + c;
 }
 
 /* torch.nn.utils.clip_grad_norm_: clip_coef = max_norm / (total_norm + 1e-6),

@@ -45,7 +45,8 @@ def test_known_answer_vs_torch_adamw(gdtype, hip_device):
 
 def _oracle_layer_step(orc, step, pieces, grads, ms, vs):
     for p, g, m, v in zip(pieces, grads, ms, vs):
-        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, g16="bf16")
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v,
+                   g16="bf16" if g.dtype == np.uint16 else None)
 
 
 def test_step_per_tensor_and_grad_views(hip_device):
@@ -63,13 +64,17 @@ def test_step_per_tensor_and_grad_views(hip_device):
     hm = [np.zeros_like(x) for x in init]
     hv = [np.zeros_like(x) for x in init]
     for step in range(1, 4):
-        grads = [torch.from_numpy(rng.normal(0, 1e-3, x.size).astype(np.float32)).bfloat16() for x in init]
-        gbits = [H.to_np_bits(g, "bf16") for g in grads]
+        grads = [torch.from_numpy(rng.normal(0, 1e-3, x.size).astype(np.float32)) for x in init]
         if step % 2:
+            # p.grad must have the param's dtype: the (f32, f32, f32) triple
+            gbits = [g.numpy().copy() for g in grads]
             for p, g, s in zip(params, grads, shapes):
                 p.grad = g.view(s).to(hip_device)
             adam.step(0)
         else:
+            # grad views carry the runtime's bf16 grads (transformer_layer.py:225,232)
+            grads = [g.bfloat16() for g in grads]
+            gbits = [H.to_np_bits(g, "bf16") for g in grads]
             adam.step_with_grad_views(0, {p: g.view(s).to(hip_device) for p, g, s in zip(params, grads, shapes)})
         _oracle_layer_step(orc, step, hp, gbits, hm, hv)
     torch.cuda.synchronize()

@@ -3,8 +3,9 @@
 Bar: fp32 p/m/v and 16-bit states bit-exact against the oracle (which is
 itself bit-exact against the reference compiled from its sources, see
 test_oracle.py); the bf16 compute copy bit-exact to RNE of the updated fp32
-master; the grad norm within 1e-12 relative of the float64 sequential sum
-(the tolerance north_star allows is 1e-6); NaN compared as a class.
+master; the grad norm within 1e-12 relative of the oracle's compensated
+float64 sum, which is the exact sum to about one binary64 ulp (the tolerance
+north_star allows is 1e-6); NaN compared as a class.
 """
 from __future__ import annotations
 
@@ -259,7 +260,9 @@ def test_clip_coef_matches_oracle_and_torch(hip_device):
         w = torch.nn.Parameter(g.clone())
         w.grad = g.clone()
         total = torch.nn.utils.clip_grad_norm_([w], max_norm)
-        assert abs(total.item() - norm.item()) <= 2e-7 * norm.item()
+        # torch reduces in fp32 on the GPU (relative error ~1e-6 at this length);
+        # ours is the float64 sum rounded once, pinned bit-exact by the oracle above
+        assert abs(total.item() - norm.item()) <= 1e-5 * norm.item()
 
 
 def test_clip_non_finite_norm_propagates(hip_device):
