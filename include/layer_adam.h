@@ -102,16 +102,27 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
                    uint16_t* p_bf16_out, const float* clip_coef, la_stream_t stream);
 
 /*
- * Grad-norm stage 1 + 2 (no counterpart in the reference, which has no
- * clipping; SlideFormer's update sits at transformer_layer.py:453-493):
- * sum of squares of g[0..n) in float64 into *sqnorm (device), added to the
- * old value when accumulate != 0.  `partials` is a caller-owned device
- * workspace of at least la_grad_sqnorm_workspace(n) bytes.
- * Deterministic for a given n and pointer alignment.
+ * Grad norm (no counterpart in the reference, which has no clipping;
+ * SlideFormer's update sits at transformer_layer.py:453-493): sum of squares
+ * of g[0..n) in float64 into *sqnorm (device), added to the old value when
+ * accumulate != 0.  Two kernels on `stream`: per-workgroup partials, then one
+ * workgroup folds them.
+ * `workspace` is caller-owned device memory of at least
+ * la_grad_sqnorm_workspace(n) bytes, 8-byte aligned, holding the partials.
+ * Calls that share a workspace must be ordered (same stream); overlapping
+ * calls race.  Deterministic for a given n and pointer alignment.
  */
 uint64_t la_grad_sqnorm_workspace(uint64_t n);
-int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, double* partials,
-                   uint64_t partials_bytes, double* sqnorm, int accumulate, la_stream_t stream);
+int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, void* workspace,
+                   uint64_t workspace_bytes, double* sqnorm, int accumulate, la_stream_t stream);
+
+/*
+ * la_grad_sqnorm whose folding kernel also writes the clip coefficient of the
+ * (accumulated) *sqnorm, as la_clip_coef computes it.  coef must not be NULL.
+ */
+int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace,
+                      uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm,
+                      float* coef, float* norm_out, la_stream_t stream);
 
 /*
  * Clip coefficient on device, torch.nn.utils.clip_grad_norm_ convention:

@@ -33,6 +33,7 @@ EXPORTED = (
     "la_adam_update",
     "la_grad_sqnorm_workspace",
     "la_grad_sqnorm",
+    "la_grad_norm_clip",
     "la_clip_coef",
 )
 
@@ -84,6 +85,8 @@ def _declare(L):
     L.la_grad_sqnorm_workspace.restype = u64
     L.la_grad_sqnorm.argtypes = [i, P, u64, P, u64, P, i, P]
     L.la_grad_sqnorm.restype = i
+    L.la_grad_norm_clip.argtypes = [i, P, u64, P, u64, P, i, f, P, P, P]
+    L.la_grad_norm_clip.restype = i
     L.la_clip_coef.argtypes = [P, f, P, P, P]
     L.la_clip_coef.restype = i
     return L

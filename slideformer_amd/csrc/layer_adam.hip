@@ -3,8 +3,15 @@
 // One pass over a layer's flat buffers reads p, g, m, v and writes p, m, v and
 // the bf16 compute copy of p: 28 algorithmic bytes per element for the hot
 // triple (fp32 p/m/v, bf16 g).  Nothing here is a contraction, so there is no
-// MFMA; the kernel is bound by HBM bandwidth.  Each lane moves 8 consecutive
-// elements per iteration with 16-byte global loads/stores.
+// MFMA; the kernel is bound by HBM bandwidth.
+//
+// Memory layout of a launch: lane L of a wave owns 4 consecutive elements, so
+// one wave instruction covers 256 consecutive elements of every stream
+// (16-byte fp32 accesses, 8-byte 16-bit accesses, all lane-contiguous).  The
+// grid is one-shot (one group of 4 per lane) up to 2^22 workgroups: on gfx950
+// the vector memory counter covers loads and stores alike, so a grid-stride
+// loop would make each trip wait for the previous trip's store acknowledgements.
+// Loads and stores carry the nontemporal hint: every byte is touched once.
 //
 // Arithmetic follows the reference CPU Adam op for op (cpu_adam.h:159-192),
 // with explicit fmaf() and this file compiled with -ffp-contract=off; fp32
@@ -12,9 +19,11 @@
 // kept.  The last n % 16 elements of a call follow the reference's scalar tail
 // (cpu_adam_impl.cpp:46-67) as its GCC build contracts it.
 //
-// The grad norm is a two-stage reduction: per-lane float64 sums, a wave64 DPP
-// reduction, LDS across the 4 waves of a workgroup, one partial per workgroup,
-// then a single workgroup folds the partials in a fixed order.
+// The grad norm is two launches: stage 1 keeps per-lane float64 sums, reduces
+// them across the wave64 with DPP and across the 4 waves of a workgroup in
+// LDS, and writes one partial per workgroup to the caller's workspace; stage 2
+// (one workgroup) folds the partials in a fixed order and, optionally, writes
+// the clip coefficient.
 
 #include <hip/hip_runtime.h>
 
@@ -27,25 +36,42 @@
 
 #include "../../include/layer_adam.h"
 
+// Update workgroup size.  One wave per workgroup: in a one-shot grid a
+// finished wave is replaced at once instead of waiting for its siblings
+// (measured on MI355X, C2 layer: 64 -> 6.17 TB/s, 128 -> 6.02, 256 -> 5.94).
 #ifndef LA_BLOCK
-#define LA_BLOCK 256
+#define LA_BLOCK 64
+#endif
+// Grad-norm workgroup size (4 waves; partials are folded in LDS first).
+#ifndef LA_NORM_BLOCK
+#define LA_NORM_BLOCK 256
 #endif
 // Upper bound on update workgroups per launch (grid-stride beyond it).
 #ifndef LA_MAX_GRID
-#define LA_MAX_GRID 8192
+#define LA_MAX_GRID (1 << 26)
 #endif
-// Workgroups of the grad-norm stage 1 (bounded so stage 2 is one workgroup).
+// Upper bound on grad-norm stage-1 workgroups (= partials folded by stage 2).
+// Measured on MI355X over a 218M-element bf16 buffer: 2048 workgroups with 2
+// groups per lane per trip read at ~6.3 TB/s; larger grids lose to the
+// single-workgroup fold.
 #ifndef LA_NORM_MAX_GRID
 #define LA_NORM_MAX_GRID 2048
 #endif
-// Groups of 8 elements each lane handles per loop trip.
-#ifndef LA_UNROLL
-#define LA_UNROLL 1
+// Groups of 4 each lane of the grad-norm kernel loads per loop trip.
+#ifndef LA_NORM_UNROLL
+#define LA_NORM_UNROLL 2
+#endif
+// Nontemporal hints on the streaming loads / stores.
+#ifndef LA_NT_LOAD
+#define LA_NT_LOAD 1
+#endif
+#ifndef LA_NT_STORE
+#define LA_NT_STORE 1
 #endif
 
 namespace {
 
-constexpr int kVec = 8;  // elements per lane per group
+constexpr int kVec = 4;  // elements per lane per group
 
 // ---------------------------------------------------------------------------
 // element types
@@ -59,8 +85,8 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as
 // round_to_nearest_even used by the fp32->bf16 copy_ (transformer_layer.py:304).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
 {
-    uint32_t u = __float_as_uint(f);
-    uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
     return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
 }
 
@@ -96,22 +122,40 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f)
     return sign | q;
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename V> __device__ __forceinline__ V vload(const void* p)
+{
+#if LA_NT_LOAD
+    return __builtin_nontemporal_load(static_cast<const V*>(p));
+#else
+    return *static_cast<const V*>(p);
+#endif
+}
+
+template <typename V> __device__ __forceinline__ void vstore(void* p, V v)
+{
+#if LA_NT_STORE
+    __builtin_nontemporal_store(v, static_cast<V*>(p));
+#else
+    *static_cast<V*>(p) = v;
+#endif
+}
+
+// 4 consecutive elements <-> 4 floats; `e` is a multiple of 4 past an aligned head.
 template <typename T> struct Io;
 
 template <> struct Io<float> {
     static constexpr int kBytes = 4;
-    __device__ __forceinline__ static void load8(const void* base, uint64_t e, float (&x)[kVec])
+    __device__ __forceinline__ static void load4(const void* base, uint64_t e, float (&x)[kVec])
     {
-        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(base) + e);
-        float4 a = q[0], b = q[1];
+        const f32x4 a = vload<f32x4>(static_cast<const float*>(base) + e);
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     }
-    __device__ __forceinline__ static void store8(void* base, uint64_t e, const float (&x)[kVec])
+    __device__ __forceinline__ static void store4(void* base, uint64_t e, const float (&x)[kVec])
     {
-        float4* q = reinterpret_cast<float4*>(static_cast<float*>(base) + e);
-        q[0] = make_float4(x[0], x[1], x[2], x[3]);
-        q[1] = make_float4(x[4], x[5], x[6], x[7]);
+        vstore<f32x4>(static_cast<float*>(base) + e, f32x4{x[0], x[1], x[2], x[3]});
     }
     __device__ __forceinline__ static float load1(const void* base, uint64_t e)
     {
@@ -125,23 +169,19 @@ template <> struct Io<float> {
 
 template <typename Conv> struct Io16 {
     static constexpr int kBytes = 2;
-    __device__ __forceinline__ static void load8(const void* base, uint64_t e, float (&x)[kVec])
+    __device__ __forceinline__ static void load4(const void* base, uint64_t e, float (&x)[kVec])
     {
-        uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + e);
-        uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[2 * j] = Conv::to_f32(w[j] & 0xffffu);
-            x[2 * j + 1] = Conv::to_f32(w[j] >> 16);
-        }
+        const u32x2 u = vload<u32x2>(static_cast<const uint16_t*>(base) + e);
+        x[0] = Conv::to_f32(u.x & 0xffffu);
+        x[1] = Conv::to_f32(u.x >> 16);
+        x[2] = Conv::to_f32(u.y & 0xffffu);
+        x[3] = Conv::to_f32(u.y >> 16);
     }
-    __device__ __forceinline__ static void store8(void* base, uint64_t e, const float (&x)[kVec])
+    __device__ __forceinline__ static void store4(void* base, uint64_t e, const float (&x)[kVec])
     {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            w[j] = Conv::from_f32(x[2 * j]) | (Conv::from_f32(x[2 * j + 1]) << 16);
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + e) = make_uint4(w[0], w[1], w[2], w[3]);
+        const uint32_t lo = Conv::from_f32(x[0]) | (Conv::from_f32(x[1]) << 16);
+        const uint32_t hi = Conv::from_f32(x[2]) | (Conv::from_f32(x[3]) << 16);
+        vstore<u32x2>(static_cast<uint16_t*>(base) + e, u32x2{lo, hi});
     }
     __device__ __forceinline__ static float load1(const void* base, uint64_t e)
     {
@@ -179,11 +219,11 @@ __device__ __forceinline__ void adam_body(float& p, float g, float& m, float& v,
     m = m * k.b1;                                            // :175
     m = __builtin_fmaf(g, k.omb1, m);                        // :176
     v = v * k.b2;                                            // :177
-    float gg = g * g;                                        // :178
+    const float gg = g * g;                                  // :178
     v = __builtin_fmaf(gg, k.omb2, v);                       // :179
     float d = __builtin_sqrtf(v);                            // :180
     d = __builtin_fmaf(d, k.bc2, k.eps);                     // :181
-    float u = m / d;                                         // :182
+    const float u = m / d;                                   // :182
     if (k.mode == 2) p = __builtin_fmaf(p, k.w_decay, p);    // :184-186
     p = __builtin_fmaf(u, k.step_size, p);                   // :188
 }
@@ -193,14 +233,14 @@ __device__ __forceinline__ void adam_body(float& p, float g, float& m, float& v,
 __device__ __forceinline__ void adam_tail(float& p, float g, float& m, float& v, const Coeffs& k)
 {
     if (k.mode == 1) g = __builtin_fmaf(p, k.wd, g);
-    float gm = g * k.omb1;
+    const float gm = g * k.omb1;
     m = __builtin_fmaf(m, k.b1, gm);
     float gg = g * g;
     gg = gg * k.omb2;
     v = __builtin_fmaf(v, k.b2, gg);
     float d = __builtin_sqrtf(v);
     d = __builtin_fmaf(d, k.bc2, k.eps);
-    float u = m / d;
+    const float u = m / d;
     if (k.mode == 2) p = __builtin_fmaf(p, k.w_decay, p);
     p = __builtin_fmaf(u, k.step_size, p);
 }
@@ -214,7 +254,7 @@ struct StepArgs {
     const float* coef;   // clip coefficient (device), may be null
     uint64_t n;
     uint64_t head;       // elements before the first aligned group
-    uint64_t nvec;       // aligned groups of 8, starting at `head`
+    uint64_t nvec;       // aligned groups of 4, starting at `head`
     uint64_t tail_start; // n - n % 16: first element of the reference's scalar tail
     Coeffs k;
 };
@@ -227,38 +267,25 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
 
-    for (uint64_t base = tid; base < a.nvec; base += stride * LA_UNROLL) {
-        float p[LA_UNROLL][kVec], g[LA_UNROLL][kVec], m[LA_UNROLL][kVec], v[LA_UNROLL][kVec];
-        bool live[LA_UNROLL];
+    for (uint64_t gi = tid; gi < a.nvec; gi += stride) {
+        const uint64_t e = a.head + gi * kVec;
+        float p[kVec], g[kVec], m[kVec], v[kVec];
+        Io<TG>::load4(a.g, e, g);
+        Io<TP>::load4(a.p, e, p);
+        Io<TS>::load4(a.m, e, m);
+        Io<TS>::load4(a.v, e, v);
 #pragma unroll
-        for (int u = 0; u < LA_UNROLL; ++u) {
-            const uint64_t gi = base + u * stride;
-            live[u] = gi < a.nvec;
-            if (live[u]) {
-                const uint64_t e = a.head + gi * kVec;
-                Io<TG>::load8(a.g, e, g[u]);
-                Io<TP>::load8(a.p, e, p[u]);
-                Io<TS>::load8(a.m, e, m[u]);
-                Io<TS>::load8(a.v, e, v[u]);
-            }
+        for (int j = 0; j < kVec; ++j) {
+            const float gj = has_coef ? g[j] * coef : g[j];
+            adam_body(p[j], gj, m[j], v[j], a.k);
         }
-#pragma unroll
-        for (int u = 0; u < LA_UNROLL; ++u) {
-            if (!live[u]) continue;
-            const uint64_t e = a.head + (base + u * stride) * kVec;
-#pragma unroll
-            for (int j = 0; j < kVec; ++j) {
-                float gj = has_coef ? g[u][j] * coef : g[u][j];
-                adam_body(p[u][j], gj, m[u][j], v[u][j], a.k);
-            }
-            Io<TP>::store8(a.p, e, p[u]);
-            Io<TS>::store8(a.m, e, m[u]);
-            Io<TS>::store8(a.v, e, v[u]);
-            if (a.out) Io<bf16_t>::store8(a.out, e, p[u]);
-        }
+        Io<TP>::store4(a.p, e, p);
+        Io<TS>::store4(a.m, e, m);
+        Io<TS>::store4(a.v, e, v);
+        if (a.out) Io<bf16_t>::store4(a.out, e, p);
     }
 
-    // Elements outside the aligned groups: [0, head) and [head + 8*nvec, n).
+    // Elements outside the aligned groups: [0, head) and [head + 4*nvec, n).
     const uint64_t vec_end = a.head + a.nvec * kVec;
     const uint64_t nscalar = a.head + (a.n - vec_end);
     for (uint64_t s = tid; s < nscalar; s += stride) {
@@ -307,10 +334,11 @@ __device__ __forceinline__ double wave_sum_f64(double x)
     return x;
 }
 
-// Sum over the workgroup; valid in thread 0.
+// Sum over the workgroup; valid in thread 0.  Ends with every wave past the
+// barrier, so it may be called again in the same kernel.
 __device__ __forceinline__ double block_sum_f64(double x)
 {
-    __shared__ double part[LA_BLOCK / 64];
+    __shared__ double part[LA_NORM_BLOCK / 64];
     x = wave_sum_f64(x);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 63) part[wave] = x;
@@ -318,54 +346,92 @@ __device__ __forceinline__ double block_sum_f64(double x)
     double t = 0.0;
     if (threadIdx.x == 0) {
 #pragma unroll
-        for (int w = 0; w < LA_BLOCK / 64; ++w) t += part[w];
+        for (int w = 0; w < LA_NORM_BLOCK / 64; ++w) t += part[w];
     }
+    __syncthreads();
     return t;
 }
 
-template <typename TG>
-__global__ __launch_bounds__(LA_BLOCK) void la_sqnorm_stage1(const void* g, uint64_t n, uint64_t head,
-                                                             uint64_t nvec, double* partials)
+// torch.nn.utils.clip_grad_norm_: coef = min(1, max_norm / (norm + 1e-6)) in fp32.
+__device__ __forceinline__ void write_clip(double sq, float max_norm, float* coef, float* norm_out)
 {
-    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
+    const float norm = static_cast<float>(__builtin_sqrt(sq));
+    const float c = max_norm / (norm + 1e-6f);
+    *coef = (c < 1.0f || c != c) ? c : 1.0f;
+    if (norm_out) *norm_out = norm;
+}
+
+struct NormArgs {
+    const void* g;
+    uint64_t n, head, nvec;
+    double* partials;     // one slot per stage-1 workgroup
+    double* sqnorm;
+    int32_t accumulate;
+    float max_norm;
+    float* coef;          // may be null: then only *sqnorm is written
+    float* norm_out;      // may be null
+};
+
+template <typename TG>
+__global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
+{
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_NORM_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_NORM_BLOCK;
     double acc = 0.0;
-    for (uint64_t gi = tid; gi < nvec; gi += stride) {
+    uint64_t gi = tid;
+    for (; gi + (LA_NORM_UNROLL - 1) * stride < a.nvec; gi += LA_NORM_UNROLL * stride) {
+        float x[LA_NORM_UNROLL][kVec];
+#pragma unroll
+        for (int u = 0; u < LA_NORM_UNROLL; ++u) Io<TG>::load4(a.g, a.head + (gi + u * stride) * kVec, x[u]);
+#pragma unroll
+        for (int u = 0; u < LA_NORM_UNROLL; ++u)
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                const double d = static_cast<double>(x[u][j]);
+                acc = __builtin_fma(d, d, acc);
+            }
+    }
+    for (; gi < a.nvec; gi += stride) {
         float x[kVec];
-        Io<TG>::load8(g, head + gi * kVec, x);
+        Io<TG>::load4(a.g, a.head + gi * kVec, x);
 #pragma unroll
         for (int j = 0; j < kVec; ++j) {
             const double d = static_cast<double>(x[j]);
             acc = __builtin_fma(d, d, acc);
         }
     }
-    const uint64_t vec_end = head + nvec * kVec;
-    const uint64_t nscalar = head + (n - vec_end);
+    const uint64_t vec_end = a.head + a.nvec * kVec;
+    const uint64_t nscalar = a.head + (a.n - vec_end);
     for (uint64_t s = tid; s < nscalar; s += stride) {
-        const uint64_t e = s < head ? s : vec_end + (s - head);
-        const double d = static_cast<double>(Io<TG>::load1(g, e));
+        const uint64_t e = s < a.head ? s : vec_end + (s - a.head);
+        const double d = static_cast<double>(Io<TG>::load1(a.g, e));
         acc = __builtin_fma(d, d, acc);
     }
+
     const double t = block_sum_f64(acc);
-    if (threadIdx.x == 0) partials[blockIdx.x] = t;
+    if (threadIdx.x == 0) a.partials[blockIdx.x] = t;
 }
 
-__global__ __launch_bounds__(LA_BLOCK) void la_sqnorm_stage2(const double* partials, uint32_t count,
-                                                             double* sqnorm, int accumulate)
+// Stage 2, one workgroup: fold the stage-1 partials in a fixed order.  The
+// kernel boundary makes every partial visible: a single-launch "last
+// workgroup" fold would need an agent-scope release per workgroup, which on
+// gfx950 writes back the whole per-XCD L2 each time.
+__global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_finish(NormArgs a, uint32_t nparts)
 {
-    double acc = 0.0;
-    for (uint32_t i = threadIdx.x; i < count; i += LA_BLOCK) acc += partials[i];
-    const double t = block_sum_f64(acc);
-    if (threadIdx.x == 0) *sqnorm = accumulate ? *sqnorm + t : t;
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x; i < nparts; i += LA_NORM_BLOCK) s += a.partials[i];
+    const double total = block_sum_f64(s);
+    if (threadIdx.x == 0) {
+        const double sq = a.accumulate ? *a.sqnorm + total : total;
+        *a.sqnorm = sq;
+        if (a.coef) write_clip(sq, a.max_norm, a.coef, a.norm_out);
+    }
 }
 
 __global__ void la_clip_coef_kernel(const double* sqnorm, float max_norm, float* coef, float* norm_out)
 {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const float norm = static_cast<float>(__builtin_sqrt(*sqnorm));
-    const float c = max_norm / (norm + 1e-6f);
-    *coef = (c < 1.0f || c != c) ? c : 1.0f;
-    if (norm_out) *norm_out = norm;
+    write_clip(*sqnorm, max_norm, coef, norm_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -387,56 +453,38 @@ std::unordered_map<int, HostState> g_states;
 int elem_bytes(int dt) { return dt == LA_F32 ? 4 : 2; }
 bool dt_valid(int dt) { return dt == LA_F32 || dt == LA_BF16 || dt == LA_F16; }
 
-// The nine (param, grad, state) triples the reference registers,
-// cpu_adam_impl.cpp:181-189.
-bool triple_registered(int p, int g, int s)
-{
-    if (p == LA_F32) return s == LA_F32;                                   // (f32, f32|bf16|f16, f32)
-    if (p == LA_BF16) return g != LA_F16 && (s == LA_F32 || (s == LA_BF16 && g == LA_BF16));
-    /* p == LA_F16 */ return g != LA_BF16 && (s == LA_F32 || (s == LA_F16 && g == LA_F16));
-}
-
-// First element index h in [0, 8) at which every pointer is 16-byte aligned,
-// or -1 when the pointers disagree in phase.
+// First element index h in [0, 4) at which every pointer is aligned to a full
+// group (4 elements: 16 bytes for fp32, 8 bytes for 16-bit types), or -1 when
+// the pointers disagree in phase.
 int common_head(const uintptr_t* addr, const int* bytes, int count)
 {
     for (int h = 0; h < kVec; ++h) {
         bool ok = true;
-        for (int i = 0; i < count && ok; ++i) ok = ((addr[i] + static_cast<uintptr_t>(h) * bytes[i]) & 15u) == 0;
+        for (int i = 0; i < count && ok; ++i) {
+            const uintptr_t align = static_cast<uintptr_t>(kVec * bytes[i]);
+            ok = ((addr[i] + static_cast<uintptr_t>(h) * bytes[i]) % align) == 0;
+        }
         if (ok) return h;
     }
     return -1;
 }
 
-int g_cu_count = 0;
-
-int cu_count()
+uint32_t grid_for(uint64_t work, uint64_t block, uint64_t cap)
 {
-    if (g_cu_count > 0) return g_cu_count;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 256;
-    g_cu_count = cus;
-    return cus;
-}
-
-uint32_t update_grid(uint64_t work)
-{
-    uint64_t blocks = (work + LA_BLOCK - 1) / LA_BLOCK;
+    uint64_t blocks = (work + block - 1) / block;
     if (blocks < 1) blocks = 1;
-    if (blocks > LA_MAX_GRID) blocks = LA_MAX_GRID;
+    if (blocks > cap) blocks = cap;
     return static_cast<uint32_t>(blocks);
 }
 
 uint32_t norm_grid(uint64_t n)
 {
     const uint64_t groups = (n + kVec - 1) / kVec;
-    uint64_t blocks = (groups + LA_BLOCK - 1) / LA_BLOCK;
-    if (blocks < 1) blocks = 1;
-    if (blocks > LA_NORM_MAX_GRID) blocks = LA_NORM_MAX_GRID;
-    return static_cast<uint32_t>(blocks);
+    return grid_for((groups + LA_NORM_UNROLL - 1) / LA_NORM_UNROLL, LA_NORM_BLOCK, LA_NORM_MAX_GRID);
 }
+
+// workspace: norm_grid(n) doubles of stage-1 partials
+uint64_t norm_workspace_bytes(uint64_t n) { return static_cast<uint64_t>(norm_grid(n)) * sizeof(double); }
 
 int hip_rc(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
 
@@ -444,29 +492,37 @@ template <typename TP, typename TG, typename TS>
 int launch_step(const StepArgs& a, hipStream_t stream)
 {
     const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-    const uint64_t work = a.nvec > nscalar ? (a.nvec + LA_UNROLL - 1) / LA_UNROLL : nscalar;
-    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(update_grid(work)), dim3(LA_BLOCK), 0, stream, a);
+    const uint64_t work = a.nvec > nscalar ? a.nvec : nscalar;
+    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK), 0, stream,
+                       a);
     return hip_rc(hipGetLastError());
 }
 
-template <typename TP, typename TG>
-int dispatch_s(int s_dt, const StepArgs& a, hipStream_t st)
+// The nine (param, grad, state) triples the reference registers,
+// cpu_adam_impl.cpp:181-189; nothing else is instantiated.
+int dispatch_step(int p, int g, int s, const StepArgs& a, hipStream_t st)
 {
-    switch (s_dt) {
-    case LA_F32: return launch_step<TP, TG, float>(a, st);
-    case LA_BF16: return launch_step<TP, TG, bf16_t>(a, st);
-    default: return launch_step<TP, TG, f16_t>(a, st);
+    if (p == LA_F32 && s == LA_F32) {
+        if (g == LA_BF16) return launch_step<float, bf16_t, float>(a, st);
+        if (g == LA_F32) return launch_step<float, float, float>(a, st);
+        if (g == LA_F16) return launch_step<float, f16_t, float>(a, st);
+    } else if (p == LA_BF16) {
+        if (g == LA_BF16 && s == LA_F32) return launch_step<bf16_t, bf16_t, float>(a, st);
+        if (g == LA_F32 && s == LA_F32) return launch_step<bf16_t, float, float>(a, st);
+        if (g == LA_BF16 && s == LA_BF16) return launch_step<bf16_t, bf16_t, bf16_t>(a, st);
+    } else if (p == LA_F16) {
+        if (g == LA_F16 && s == LA_F32) return launch_step<f16_t, f16_t, float>(a, st);
+        if (g == LA_F32 && s == LA_F32) return launch_step<f16_t, float, float>(a, st);
+        if (g == LA_F16 && s == LA_F16) return launch_step<f16_t, f16_t, f16_t>(a, st);
     }
+    return LA_EDTYPE;
 }
 
-template <typename TP>
-int dispatch_g(int g_dt, int s_dt, const StepArgs& a, hipStream_t st)
+bool triple_registered(int p, int g, int s)
 {
-    switch (g_dt) {
-    case LA_F32: return dispatch_s<TP, float>(s_dt, a, st);
-    case LA_BF16: return dispatch_s<TP, bf16_t>(s_dt, a, st);
-    default: return dispatch_s<TP, f16_t>(s_dt, a, st);
-    }
+    if (p == LA_F32) return s == LA_F32;
+    if (p == LA_BF16) return g != LA_F16 && (s == LA_F32 || (s == LA_BF16 && g == LA_BF16));
+    return g != LA_BF16 && (s == LA_F32 || (s == LA_F16 && g == LA_F16));
 }
 
 void derive_scalars(HostState& s, uint64_t step, float lr, float b1, float b2, float eps, float wd,
@@ -515,6 +571,48 @@ void derive_scalars(HostState& s, uint64_t step, float lr, float b1, float b2, f
     out->beta2_t = s.betta2_t;
     out->bias_correction1 = s.bias_correction1;
     out->step = s.step;
+}
+
+int launch_norm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_t workspace_bytes,
+                double* sqnorm, int accumulate, float max_norm, float* coef, float* norm_out, hipStream_t st)
+{
+    if (!dt_valid(g_dtype)) return LA_EDTYPE;
+    if (!sqnorm || !workspace) return LA_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(sqnorm) & 7u) || (reinterpret_cast<uintptr_t>(workspace) & 7u)) return LA_EINVAL;
+    if (coef && (reinterpret_cast<uintptr_t>(coef) & 3u)) return LA_EINVAL;
+    if (norm_out && (reinterpret_cast<uintptr_t>(norm_out) & 3u)) return LA_EINVAL;
+    if (n > 0 && !g) return LA_EINVAL;
+    const int gb = elem_bytes(g_dtype);
+    if (reinterpret_cast<uintptr_t>(g) % static_cast<uintptr_t>(gb)) return LA_EINVAL;
+    if (workspace_bytes < norm_workspace_bytes(n)) return LA_EINVAL;
+
+    NormArgs a;
+    const uint32_t grid = norm_grid(n);
+    a.g = g;
+    a.n = n;
+    a.head = 0;
+    a.nvec = 0;
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(g);
+    const int h = n > 0 ? common_head(&addr, &gb, 1) : -1;
+    if (h >= 0 && static_cast<uint64_t>(h) < n) {
+        a.head = static_cast<uint64_t>(h);
+        a.nvec = (n - a.head) / kVec;
+    }
+    a.partials = static_cast<double*>(workspace);
+    a.sqnorm = sqnorm;
+    a.accumulate = accumulate ? 1 : 0;
+    a.max_norm = max_norm;
+    a.coef = coef;
+    a.norm_out = norm_out;
+    switch (g_dtype) {
+    case LA_F32: hipLaunchKernelGGL(la_sqnorm_kernel<float>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    case LA_BF16: hipLaunchKernelGGL(la_sqnorm_kernel<bf16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    default: hipLaunchKernelGGL(la_sqnorm_kernel<f16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    }
+    const int rc = hip_rc(hipGetLastError());
+    if (rc != LA_OK) return rc;
+    hipLaunchKernelGGL(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);
+    return hip_rc(hipGetLastError());
 }
 
 }  // namespace
@@ -621,13 +719,7 @@ int la_adamw_step(const la_scalars_t* sc, int p_dtype, void* p, int g_dtype, con
     a.k.w_decay = sc->w_decay;
     a.k.wd = sc->weight_decay;
     a.k.mode = sc->decay_mode;
-
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    switch (p_dtype) {
-    case LA_F32: return dispatch_g<float>(g_dtype, s_dtype, a, st);
-    case LA_BF16: return dispatch_g<bf16_t>(g_dtype, s_dtype, a, st);
-    default: return dispatch_g<f16_t>(g_dtype, s_dtype, a, st);
-    }
+    return dispatch_step(p_dtype, g_dtype, s_dtype, a, static_cast<hipStream_t>(stream));
 }
 
 int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
@@ -642,43 +734,22 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
     return la_adamw_step(&sc, p_dtype, p, g_dtype, g, s_dtype, m, v, n, p_bf16_out, clip_coef, stream);
 }
 
-uint64_t la_grad_sqnorm_workspace(uint64_t n) { return static_cast<uint64_t>(norm_grid(n)) * sizeof(double); }
+uint64_t la_grad_sqnorm_workspace(uint64_t n) { return norm_workspace_bytes(n); }
 
-int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, double* partials, uint64_t partials_bytes,
+int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_t workspace_bytes,
                    double* sqnorm, int accumulate, la_stream_t stream)
 {
-    if (!dt_valid(g_dtype)) return LA_EDTYPE;
-    if (!sqnorm || !partials) return LA_EINVAL;
-    if ((reinterpret_cast<uintptr_t>(sqnorm) & 7u) || (reinterpret_cast<uintptr_t>(partials) & 7u)) return LA_EINVAL;
-    if (n > 0 && !g) return LA_EINVAL;
-    const int gb = elem_bytes(g_dtype);
-    if (reinterpret_cast<uintptr_t>(g) % static_cast<uintptr_t>(gb)) return LA_EINVAL;
-    const uint32_t grid = norm_grid(n);
-    if (partials_bytes < static_cast<uint64_t>(grid) * sizeof(double)) return LA_EINVAL;
+    return launch_norm(g_dtype, g, n, workspace, workspace_bytes, sqnorm, accumulate, 0.0f, nullptr, nullptr,
+                       static_cast<hipStream_t>(stream));
+}
 
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(g);
-    const int h = common_head(&addr, &gb, 1);
-    uint64_t head = 0, nvec = 0;
-    if (h >= 0 && static_cast<uint64_t>(h) < n) {
-        head = static_cast<uint64_t>(h);
-        nvec = (n - head) / kVec;
-    }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    switch (g_dtype) {
-    case LA_F32:
-        hipLaunchKernelGGL(la_sqnorm_stage1<float>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
-        break;
-    case LA_BF16:
-        hipLaunchKernelGGL(la_sqnorm_stage1<bf16_t>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
-        break;
-    default:
-        hipLaunchKernelGGL(la_sqnorm_stage1<f16_t>, dim3(grid), dim3(LA_BLOCK), 0, st, g, n, head, nvec, partials);
-        break;
-    }
-    int rc = hip_rc(hipGetLastError());
-    if (rc != LA_OK) return rc;
-    hipLaunchKernelGGL(la_sqnorm_stage2, dim3(1), dim3(LA_BLOCK), 0, st, partials, grid, sqnorm, accumulate);
-    return hip_rc(hipGetLastError());
+int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_t workspace_bytes,
+                      double* sqnorm, int accumulate, float max_norm, float* coef, float* norm_out,
+                      la_stream_t stream)
+{
+    if (!coef) return LA_EINVAL;
+    return launch_norm(g_dtype, g, n, workspace, workspace_bytes, sqnorm, accumulate, max_norm, coef, norm_out,
+                       static_cast<hipStream_t>(stream));
 }
 
 int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out, la_stream_t stream)

@@ -82,18 +82,19 @@ def _unsupported(p, g, s) -> RuntimeError:
 
 
 class _ClipWorkspace:
-    """Per-device scratch for the grad-norm reduction (owned here, not by the library)."""
+    """Per-device scratch for the grad-norm reduction (owned here, not by the library):
+    the per-workgroup partials and the float64 sum of squares."""
 
     def __init__(self, device):
         self.device = device
-        self.partials = torch.empty(0, dtype=torch.float64, device=device)
+        self.buf = torch.zeros(0, dtype=torch.float64, device=device)
         self.sqnorm = torch.zeros(1, dtype=torch.float64, device=device)
 
     def ensure(self, nbytes: int) -> torch.Tensor:
         need = max(1, (nbytes + 7) // 8)
-        if self.partials.numel() < need:
-            self.partials = torch.empty(need, dtype=torch.float64, device=self.device)
-        return self.partials
+        if self.buf.numel() < need:
+            self.buf = torch.zeros(need, dtype=torch.float64, device=self.device)
+        return self.buf
 
 
 class LayerAdam:
@@ -501,22 +502,27 @@ class LayerAdam:
         ws = self._clip_ws.get(device)
         if ws is None:
             ws = self._clip_ws[device] = _ClipWorkspace(device)
+        for g in grads:
+            if g.device != device:
+                raise RuntimeError("all grads must be on one device")
+            if not g.is_contiguous():
+                raise RuntimeError("grads must be contiguous")
+            if g.dtype not in _DTYPE_CODE:
+                raise RuntimeError(f"unsupported grad dtype {g.dtype}")
         with torch.cuda.device(device):
             handle = _stream_handle(stream, device)
             coef = torch.empty(1, dtype=torch.float32, device=device)
             norm = torch.empty(1, dtype=torch.float32, device=device)
+            work = ws.ensure(max(self.lib.la_grad_sqnorm_workspace(g.numel()) for g in grads))
+            last = len(grads) - 1
             for i, g in enumerate(grads):
-                if g.device != device:
-                    raise RuntimeError("all grads must be on one device")
-                if not g.is_contiguous():
-                    raise RuntimeError("grads must be contiguous")
-                if g.dtype not in _DTYPE_CODE:
-                    raise RuntimeError(f"unsupported grad dtype {g.dtype}")
-                nbytes = self.lib.la_grad_sqnorm_workspace(g.numel())
-                part = ws.ensure(nbytes)
-                _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(part),
-                                                   part.numel() * 8, _ptr(ws.sqnorm), int(i > 0), handle),
-                           "la_grad_sqnorm")
-            _lib.check(self.lib.la_clip_coef(_ptr(ws.sqnorm), float(max_norm), _ptr(coef), _ptr(norm),
-                                             handle), "la_clip_coef")
+                if i < last:
+                    rc = self.lib.la_grad_sqnorm(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
+                                                 work.numel() * 8, _ptr(ws.sqnorm), int(i > 0), handle)
+                else:
+                    # the last buffer also writes the coefficient, in the same launch
+                    rc = self.lib.la_grad_norm_clip(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
+                                                    work.numel() * 8, _ptr(ws.sqnorm), int(i > 0),
+                                                    float(max_norm), _ptr(coef), _ptr(norm), handle)
+                _lib.check(rc, "la_grad_sqnorm")
         return coef, norm

@@ -60,7 +60,8 @@ def sqnorm(g: torch.Tensor, accumulate_into: torch.Tensor | None = None, stream=
     """Sum of squares of a device grad buffer in float64 (device scalar)."""
     L = _lib.load()
     kinds = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
-    ws = torch.empty(max(1, L.la_grad_sqnorm_workspace(g.numel()) // 8), dtype=torch.float64,
+    # the workspace's ticket word must start at zero
+    ws = torch.zeros(max(1, L.la_grad_sqnorm_workspace(g.numel()) // 8), dtype=torch.float64,
                      device=g.device)
     out = accumulate_into if accumulate_into is not None else torch.zeros(1, dtype=torch.float64,
                                                                          device=g.device)
@@ -78,3 +79,20 @@ def clip_coef(sq: torch.Tensor, max_norm: float):
     _lib.check(L.la_clip_coef(sq.data_ptr(), float(max_norm), coef.data_ptr(), norm.data_ptr(),
                               torch.cuda.current_stream(sq.device).cuda_stream), "la_clip_coef")
     return coef, norm
+
+
+def norm_clip(g: torch.Tensor, max_norm: float, ws: torch.Tensor | None = None):
+    """One-launch sum of squares + clip coefficient (la_grad_norm_clip)."""
+    L = _lib.load()
+    kinds = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+    if ws is None:
+        ws = torch.zeros(max(1, L.la_grad_sqnorm_workspace(g.numel()) // 8), dtype=torch.float64,
+                         device=g.device)
+    sq = torch.zeros(1, dtype=torch.float64, device=g.device)
+    coef = torch.empty(1, dtype=torch.float32, device=g.device)
+    norm = torch.empty(1, dtype=torch.float32, device=g.device)
+    _lib.check(L.la_grad_norm_clip(CODE[kinds[g.dtype]], g.data_ptr(), g.numel(), ws.data_ptr(),
+                                   ws.numel() * 8, sq.data_ptr(), 0, float(max_norm), coef.data_ptr(),
+                                   norm.data_ptr(), torch.cuda.current_stream(g.device).cuda_stream),
+               "la_grad_norm_clip")
+    return sq, coef, norm

@@ -106,15 +106,18 @@ def test_error_codes_without_launch():
     assert L.la_adamw_step(ctypes.byref(sc), 0, 0x1001, 1, 0x2000, 0, 0x3000, 0x4000, 5, None, None,
                            None) == _lib.LA_EINVAL
     assert L.la_grad_sqnorm(1, None, 10, None, 0, None, 0, None) == _lib.LA_EINVAL
+    assert L.la_grad_norm_clip(1, None, 10, None, 0, None, 0, 1.0, None, None, None) == _lib.LA_EINVAL
     assert L.la_clip_coef(None, 1.0, None, None, None) == _lib.LA_EINVAL
     assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
 
 
 def test_grad_sqnorm_workspace_is_bounded():
+    """one float64 partial per stage-1 workgroup; the grid is capped so the
+    folding workgroup reads a bounded number of partials."""
     L = _lib.load()
-    assert L.la_grad_sqnorm_workspace(0) == 8
-    assert L.la_grad_sqnorm_workspace(1) == 8
-    assert L.la_grad_sqnorm_workspace(8 * 256 * 3) == 3 * 8
-    # bounded by the stage-1 grid cap, so stage 2 is one workgroup
-    assert L.la_grad_sqnorm_workspace(1 << 40) == L.la_grad_sqnorm_workspace(1 << 35)
-    assert L.la_grad_sqnorm_workspace(1 << 40) <= 64 * 1024
+    sizes = (0, 1, 7, 4096, 4097, 8 * 256 * 3, 10**6, 218_112_000, 1 << 40)
+    ws = [L.la_grad_sqnorm_workspace(n) for n in sizes]
+    assert ws[0] == ws[1] == 8                      # one workgroup
+    assert all(w % 8 == 0 and w >= 8 for w in ws)
+    assert ws == sorted(ws)                         # non-decreasing in n
+    assert ws[-1] == L.la_grad_sqnorm_workspace(1 << 35) <= 64 * 1024   # capped

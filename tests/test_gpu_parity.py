@@ -277,6 +277,28 @@ def test_clip_non_finite_norm_propagates(hip_device):
     assert np.isnan(norm.item()) and np.isnan(coef.item())
 
 
+def test_fused_norm_clip_reuses_workspace(hip_device):
+    """la_grad_norm_clip writes sqnorm, norm and coef; back-to-back calls of
+    different sizes (and so different grids) on one workspace stay exact."""
+    L = H._lib.load()
+    big = 16 * 1024 * 1024 + 3
+    ws = torch.zeros(L.la_grad_sqnorm_workspace(big) // 8 + 1, dtype=torch.float64, device=hip_device)
+    rng = np.random.default_rng(12)
+    for n in (big, 5, 300_001, big, 1, 4096):
+        g = torch.from_numpy(rng.normal(0, 1e-2, n).astype(np.float32)).bfloat16()
+        sq, coef, norm = H.norm_clip(g.to(hip_device), 1.0, ws=ws)
+        exact = O.grad_sqnorm(H.to_np_bits(g, "bf16"), "bf16")
+        assert abs(sq.item() - exact) <= 1e-12 * exact
+        c_ref, n_ref = O.clip_coef(sq.item(), 1.0)
+        assert coef.item() == np.float32(c_ref) and norm.item() == np.float32(n_ref)
+
+
+def test_norm_of_empty_buffer(hip_device):
+    g = torch.zeros(0, dtype=torch.bfloat16, device=hip_device)
+    sq, coef, norm = H.norm_clip(g, 1.0)
+    assert sq.item() == 0.0 and norm.item() == 0.0 and coef.item() == 1.0
+
+
 # ---------------------------------------------------------------------------
 # configs C2 and C4 at full size
 # ---------------------------------------------------------------------------
