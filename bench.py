@@ -120,6 +120,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU-baseline timing (0 disables it)")
     ap.add_argument("--no-clip", action="store_true", help="time the update alone (no norm pass)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before timing, run one torch fp32 copy_ of this many MiB: a plain copy "
+                         "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -169,6 +172,15 @@ def main():
         one_step(t)
     torch.cuda.synchronize()
     log(f"warm-up done ({5 + args.warmup} steps)")
+    if args.calibrate_copy_mib > 0:
+        nf = args.calibrate_copy_mib * 1024 * 1024 // 4
+        src = torch.ones(nf, device=dev)
+        dst = torch.empty(nf, device=dev)
+        torch.cuda.synchronize()
+        torch.mul(src, 2.0, out=dst)  # one elementwise kernel (a same-dtype copy_ would be a DMA)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calibrate_copy_mib} MiB read + {args.calibrate_copy_mib} MiB written")
+        del src, dst
 
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
