@@ -112,6 +112,121 @@ def cpu_baseline(n: int, budget_s: float):
     }
 
 
+C5_LAYER = [12288 * 3 * 12288, 3 * 12288, 12288 * 12288, 12288, 12288 * 49152, 49152, 49152 * 12288, 12288,
+            12288, 12288, 12288, 12288]  # qkv(+b), o(+b), fc1(+b), fc2(+b), 2 LayerNorms (w, b)
+
+
+def streamed(args):
+    """Configs C5 (one 100B-class dense layer) / C3-shaped layers with fp32 state in
+    pinned host RAM, streamed through HBM by the native chunk pipeline.  Reports
+    the streamed step rate, the effective H2D/D2H GB/s, the isolated rates of
+    each stage and the overlap (sum of isolated times / wall)."""
+    import ctypes
+
+    import torch
+
+    from slideformer_amd import LayerAdam, _lib
+    from slideformer_amd.layer_adam import HostStreamer
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.streamed == "c5":
+        n, chunk, slots, lr, gstd = sum(C5_LAYER), 64 * 1024 * 1024, 2, 6e-6, 5e-4
+        workload = ("C5: one 100B-class dense layer (hidden 12288, FFN 49152, biases), 1,812,099,072 params; "
+                    "fp32 p/m/v in pinned host RAM, 256 MB double-buffered chunks; bf16 grads and bf16 copy in HBM")
+    else:
+        n, chunk, slots, lr, gstd = sum(LLAMA8B_LAYER), 16 * 1024 * 1024, 3, 1e-5, 1e-3
+        workload = ("C3 layer: one Llama-3.1-8B-shaped layer (218,112,000 params) of the streamed model; "
+                    "fp32 p/m/v in pinned host RAM, 64 MB chunks x 3 slots; bf16 grads and bf16 copy in HBM")
+    assert n % 16 == 0
+    log(f"streamed {args.streamed}: n={n}, chunk={chunk}, slots={slots}")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(50)
+    host = []
+    for std in (0.02, 0.0, 0.0):
+        t = torch.empty(n, dtype=torch.float32, pin_memory=True)
+        piece = 256 * 1024 * 1024
+        for lo in range(0, n, piece):
+            hi = min(n, lo + piece)
+            src = torch.randn(hi - lo, generator=gen, device=dev) * std if std else torch.zeros(hi - lo, device=dev)
+            t[lo:hi].copy_(src)
+        host.append(t)
+    p, m, v = host
+    g = (torch.randn(n, generator=gen, device=dev) * gstd).bfloat16()
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    log("pinned state allocated and initialised")
+
+    adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots)
+    walls = []
+    t = 0
+    for i in range(args.warmup + args.steps):
+        t += 1
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=t), bf16_out=out)
+        st = adam.last_stream_stats
+        if i >= args.warmup:
+            walls.append(st.wall_ms)
+    wall = sum(walls) / len(walls)
+    h2d_bytes, d2h_bytes = st.h2d_bytes, st.d2h_bytes
+
+    # isolated stages: the same copies alone, and the update alone on resident buffers
+    stream = torch.cuda.current_stream(dev)
+    dbuf = torch.empty(chunk, dtype=torch.float32, device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, reps=2):
+        fn()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def h2d_only():
+        for arr in (p, m, v):
+            for lo in range(0, n, chunk):
+                hi = min(n, lo + chunk)
+                dbuf[:hi - lo].copy_(arr[lo:hi], non_blocking=True)
+
+    def d2h_only():
+        for arr in (p, m, v):
+            for lo in range(0, n, chunk):
+                hi = min(n, lo + chunk)
+                arr[lo:hi].copy_(dbuf[:hi - lo], non_blocking=True)
+
+    t_h2d = timed(h2d_only)
+    t_d2h = timed(d2h_only)
+    del dbuf
+    pd, md, vd = (x.to(dev) for x in (p, m, v))
+    t_comp = timed(lambda: adam.step_chunk(pd, g, md, vd, dict(adam.defaults, step=t + 1), bf16_out=out))
+    del pd, md, vd
+    res = {
+        "metric": "streamed LayerAdam step (host-resident fp32 state), Gparams/s",
+        "value": round(n / (wall * 1e-3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall, 3),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots},
+        "h2d_gbs_effective": round(h2d_bytes / (wall * 1e-3) / 1e9, 2),
+        "d2h_gbs_effective": round(d2h_bytes / (wall * 1e-3) / 1e9, 2),
+        "h2d_gbs_isolated": round(h2d_bytes / (t_h2d * 1e-3) / 1e9, 2),
+        "d2h_gbs_isolated": round(d2h_bytes / (t_d2h * 1e-3) / 1e9, 2),
+        "isolated_ms": {"h2d": round(t_h2d, 3), "update": round(t_comp, 3), "d2h": round(t_d2h, 3)},
+        "overlap": round((t_h2d + t_d2h + t_comp) / wall, 3),
+        "stream_spans_ms": {"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
+                            "d2h": round(st.d2h_ms, 3)},
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,6 +238,8 @@ def main():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, run one torch fp32 copy_ of this many MiB: a plain copy "
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
+    ap.add_argument("--streamed", choices=["c5", "c3"], default=None,
+                    help="instead of C2: stream host-resident state through HBM (prints its own JSON line)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -138,6 +255,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
+    if args.streamed:
+        streamed(args)
+        return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     n = sum(LLAMA8B_LAYER)

@@ -132,6 +132,50 @@ int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace,
 int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out,
                  la_stream_t stream);
 
+/*
+ * Host <-> HBM streaming of the step, for state that lives in host RAM.
+ * Replaces the runtime's chunk pipeline around the update: CPU fp32->bf16
+ * cast + H2D (transformer_layer.py:297-305), grad D2H in chunks with
+ * per-chunk events (:343-422) and the update thread consuming them (:453-493).
+ * Here p, m, v are copied in, updated on the GPU and copied back, chunk by
+ * chunk, on three HIP streams (H2D, compute, D2H) so that transfers in both
+ * directions overlap the update of other chunks.
+ *
+ * la_pipeline_create: chunk_elems is rounded down to a multiple of 16 (only
+ *   the last chunk of a call then holds the reference's scalar tail); 1..16
+ *   staging slots.  Creates the streams and events; allocates no memory.
+ * la_pipeline_workspace_bytes: device staging bytes the caller must provide
+ *   (256-byte aligned) for the given element types and placements.
+ * la_pipeline_step: one reference adam_update over n elements whose p, m, v
+ *   live in host memory (pinned for full speed).  g is on the host when
+ *   g_on_host, else on the device; the bf16 copy `out` (nullable) goes to the
+ *   host when out_on_host, else stays on the device.  Work queued on `after`
+ *   before the call runs first; work queued on `after` later sees the
+ *   result.  synchronize != 0 (or stats != NULL) waits for completion.
+ *   One pipeline object must not be used by two threads at once.
+ */
+typedef struct la_pipeline la_pipeline_t;
+
+typedef struct {
+    float wall_ms;      /* first H2D start .. last D2H end */
+    float h2d_ms;       /* span of the H2D stream (includes waits for free slots) */
+    float compute_ms;   /* span of the compute stream */
+    float d2h_ms;       /* span of the D2H stream */
+    uint64_t h2d_bytes;
+    uint64_t d2h_bytes;
+    uint32_t chunks;
+} la_pipeline_stats_t;
+
+uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtype, int g_dtype,
+                                     int s_dtype, int g_on_host, int out_on_host);
+int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out);
+int la_pipeline_destroy(la_pipeline_t* pl);
+int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host,
+                     int g_dtype, const void* g, int g_on_host, int s_dtype, void* m_host,
+                     void* v_host, uint64_t n, uint16_t* out, int out_on_host,
+                     const float* clip_coef, void* workspace, uint64_t workspace_bytes,
+                     la_stream_t after, int synchronize, la_pipeline_stats_t* stats);
+
 #ifdef __cplusplus
 }
 #endif

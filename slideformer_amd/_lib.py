@@ -35,7 +35,25 @@ EXPORTED = (
     "la_grad_sqnorm",
     "la_grad_norm_clip",
     "la_clip_coef",
+    "la_pipeline_workspace_bytes",
+    "la_pipeline_create",
+    "la_pipeline_destroy",
+    "la_pipeline_step",
 )
+
+
+class LaPipelineStats(ctypes.Structure):
+    """Mirror of ``la_pipeline_stats_t``."""
+
+    _fields_ = [
+        ("wall_ms", ctypes.c_float),
+        ("h2d_ms", ctypes.c_float),
+        ("compute_ms", ctypes.c_float),
+        ("d2h_ms", ctypes.c_float),
+        ("h2d_bytes", ctypes.c_uint64),
+        ("d2h_bytes", ctypes.c_uint64),
+        ("chunks", ctypes.c_uint32),
+    ]
 
 
 class LaScalars(ctypes.Structure):
@@ -89,6 +107,15 @@ def _declare(L):
     L.la_grad_norm_clip.restype = i
     L.la_clip_coef.argtypes = [P, f, P, P, P]
     L.la_clip_coef.restype = i
+    L.la_pipeline_workspace_bytes.argtypes = [u64, i, i, i, i, i, i]
+    L.la_pipeline_workspace_bytes.restype = u64
+    L.la_pipeline_create.argtypes = [u64, i, ctypes.POINTER(P)]
+    L.la_pipeline_create.restype = i
+    L.la_pipeline_destroy.argtypes = [P]
+    L.la_pipeline_destroy.restype = i
+    L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, i, P, P, u64, P, i, P, P, u64, P, i,
+                                   ctypes.POINTER(LaPipelineStats)]
+    L.la_pipeline_step.restype = i
     return L
 
 

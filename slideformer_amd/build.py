@@ -22,7 +22,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libslideformer_amd.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
-SOURCES = [os.path.join(CSRC, "layer_adam.hip")]
+SOURCES = [os.path.join(CSRC, "layer_adam.hip"), os.path.join(CSRC, "pipeline.hip")]
 ARCH = "gfx950"
 
 BASE_FLAGS = [

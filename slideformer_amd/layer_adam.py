@@ -10,9 +10,11 @@ the same methods (``add_layer_params``, ``step``, ``step_with_grad_views``,
 beta-power state machine of the reference runs on the host inside that library.
 
 Device tensors are updated in place, asynchronously on the current HIP stream.
-Host tensors (the reference's layout: fp32 master in CPU RAM) are staged
-through HBM in 16 Mi-element pieces and the call returns after completion, as
-the reference's CPU call does.  There is no CPU arithmetic path.
+Host tensors (the reference's layout: fp32 master and moments in CPU RAM) are
+streamed through HBM in 16 Mi-element chunks by the library's native
+three-stream pipeline (H2D / update / D2H overlapped) and the call returns
+after completion, as the reference's CPU call does; grads and the bf16 copy may
+then live on the host or on the device.  There is no CPU arithmetic path.
 
 Additions, all keyword-only so that positional signatures are unchanged:
 ``bf16_out=`` (the bf16 compute copy written in the same pass), ``clip_coef=``
@@ -50,10 +52,61 @@ SUPPORTED_TRIPLES = frozenset({
     (torch.float32, torch.float16, torch.float32),
 })
 
-# Host tensors are staged through HBM in pieces of this many elements.  A
-# multiple of 16, so that only the last piece of a call holds the reference's
-# scalar tail (the last n % 16 elements of the call).
+# Host tensors are streamed through HBM in chunks of this many elements (64 MB
+# of fp32 per state array), through HOST_STAGE_SLOTS staging slots.  A multiple
+# of 16, so that only the last chunk of a call holds the reference's scalar
+# tail (the last n % 16 elements of the call).
 HOST_STAGE_ELEMS = 16 * 1024 * 1024
+HOST_STAGE_SLOTS = 3
+
+
+class HostStreamer:
+    """One native chunk pipeline (``la_pipeline_t``) on one device, plus the
+    device staging memory it needs (allocated here, never by the library)."""
+
+    def __init__(self, device, chunk_elems: int = HOST_STAGE_ELEMS, slots: int = HOST_STAGE_SLOTS):
+        self.lib = _lib.load()
+        self.device = torch.device(device)
+        self.chunk = chunk_elems
+        self.slots = slots
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _lib.check(self.lib.la_pipeline_create(chunk_elems, slots, ctypes.byref(handle)),
+                       "la_pipeline_create")
+        self.handle = handle
+        self._ws = {}
+
+    def workspace(self, pc, gc, sc, g_on_host, out_on_host) -> torch.Tensor:
+        key = (pc, gc, sc, g_on_host, out_on_host)
+        ws = self._ws.get(key)
+        if ws is None:
+            nbytes = self.lib.la_pipeline_workspace_bytes(self.chunk, self.slots, pc, gc, sc,
+                                                          int(g_on_host), int(out_on_host))
+            ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
+            self._ws[key] = ws
+        return ws
+
+    def step(self, scalars, pc, params, gc, grads, g_on_host, sc, exp_avg, exp_avg_sq, n, bf16_out,
+             out_on_host, clip_coef, stream_handle):
+        ws = self.workspace(pc, gc, sc, g_on_host, out_on_host)
+        base = ws.data_ptr()
+        aligned = (base + 255) // 256 * 256
+        stats = _lib.LaPipelineStats()
+        rc = self.lib.la_pipeline_step(
+            self.handle, ctypes.byref(scalars), pc, params.data_ptr(), gc, grads.data_ptr(),
+            int(g_on_host), sc, exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n,
+            None if bf16_out is None else bf16_out.data_ptr(), int(out_on_host),
+            None if clip_coef is None else clip_coef.data_ptr(), aligned,
+            ws.numel() - (aligned - base), stream_handle, 1, ctypes.byref(stats))
+        _lib.check(rc, "la_pipeline_step")
+        return stats
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                self.lib.la_pipeline_destroy(self.handle)
+        except Exception:
+            pass
 
 _ids = itertools.count()
 _ids_lock = threading.Lock()
@@ -153,6 +206,9 @@ class LayerAdam:
         self.exp_avg_flat = OrderedDict()
         self.exp_avg_sq_flat = OrderedDict()
         self._clip_ws: Dict[Any, _ClipWorkspace] = {}
+        self._streamers: Dict[Any, HostStreamer] = {}
+        # la_pipeline_stats_t of the last host-state update (timings, bytes moved)
+        self.last_stream_stats = None
 
         if self.nvme_offload_fraction > 0.0:
             # layer_adam.py:92-101; the NVMe state offload is not part of this build.
@@ -302,18 +358,26 @@ class LayerAdam:
             if clip_coef.dtype != torch.float32 or clip_coef.numel() < 1 or clip_coef.device.type != 'cuda':
                 raise RuntimeError("clip_coef must be a float32 device tensor")
 
-        devs = {t.device for t in (params, grads, exp_avg, exp_avg_sq) if t is not None}
-        if bf16_out is not None:
-            devs.add(bf16_out.device)
-        if len(devs) != 1:
-            raise RuntimeError(f"params/grads/states must be on one device, got {sorted(map(str, devs))}")
-        device = devs.pop()
+        state_devs = {t.device for t in (params, exp_avg, exp_avg_sq)}
+        if len(state_devs) != 1:
+            raise RuntimeError(f"params/exp_avg/exp_avg_sq must be on one device, got "
+                               f"{sorted(map(str, state_devs))}")
+        device = state_devs.pop()
         if device.type == 'cuda':
+            others = {grads.device} | ({bf16_out.device} if bf16_out is not None else set())
+            if others != {device}:
+                raise RuntimeError(f"params/grads/states must be on one device, got "
+                                   f"{sorted(map(str, others | {device}))}")
             self._device_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
                                 grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n)
         elif device.type == 'cpu':
+            # host state: grads and the bf16 copy may be on the host or on one device
+            gpu_devs = {t.device for t in (grads, bf16_out, clip_coef) if t is not None and t.is_cuda}
+            if len(gpu_devs) > 1:
+                raise RuntimeError(f"params/grads/states must be on one device, got {sorted(map(str, gpu_devs))}")
             self._host_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
-                              grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n)
+                              grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n,
+                              gpu_devs.pop() if gpu_devs else None)
         else:
             raise RuntimeError(f"unsupported device type: {device.type}")
 
@@ -347,43 +411,25 @@ class LayerAdam:
         _lib.check(rc, "la_adam_update")
 
     def _host_update(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
-                     grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n):
-        """Host tensors: stage through HBM, update there, copy back; returns after completion."""
+                     grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n, gpu):
+        """Host state: stream it through HBM with the native chunk pipeline
+        (la_pipeline_step); returns after completion, as the reference's CPU call does."""
         if not torch.cuda.is_available():
             raise RuntimeError("LayerAdam needs a HIP device (MI355X); there is no CPU arithmetic path")
         sc = self._scalars(step, lr, beta1, beta2, eps, weight_decay, bias_correction)
         pc, gc, sc_ = self._codes(params, grads, exp_avg)
         if n == 0:
             return
-        device = self.device or torch.device('cuda', torch.cuda.current_device())
+        device = gpu or self.device or torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(device):
-            st = torch.cuda.current_stream(device) if stream is None else stream
-            handle = _stream_handle(st, device)
-            piece = min(n, HOST_STAGE_ELEMS)
-            dp = torch.empty(piece, dtype=params.dtype, device=device)
-            dg = torch.empty(piece, dtype=grads.dtype, device=device)
-            dm = torch.empty(piece, dtype=exp_avg.dtype, device=device)
-            dv = torch.empty(piece, dtype=exp_avg_sq.dtype, device=device)
-            db = torch.empty(piece, dtype=torch.bfloat16, device=device) if bf16_out is not None else None
-            cc = clip_coef.to(device) if clip_coef is not None else None
-            with torch.cuda.stream(st):
-                for cs in range(0, n, piece):
-                    ce = min(cs + piece, n)
-                    k = ce - cs
-                    dp[:k].copy_(params.view(-1)[cs:ce])
-                    dg[:k].copy_(grads.view(-1)[cs:ce])
-                    dm[:k].copy_(exp_avg.view(-1)[cs:ce])
-                    dv[:k].copy_(exp_avg_sq.view(-1)[cs:ce])
-                    rc = self.lib.la_adamw_step(
-                        ctypes.byref(sc), pc, _ptr(dp), gc, _ptr(dg), sc_, _ptr(dm), _ptr(dv), k,
-                        _ptr(db), _ptr(cc), handle)
-                    _lib.check(rc, "la_adamw_step")
-                    params.view(-1)[cs:ce].copy_(dp[:k])
-                    exp_avg.view(-1)[cs:ce].copy_(dm[:k])
-                    exp_avg_sq.view(-1)[cs:ce].copy_(dv[:k])
-                    if bf16_out is not None:
-                        bf16_out.view(-1)[cs:ce].copy_(db[:k])
-            st.synchronize()
+            streamer = self._streamers.get(device)
+            if streamer is None:
+                streamer = self._streamers[device] = HostStreamer(device)
+            g_on_host = not grads.is_cuda
+            out_on_host = bf16_out is not None and not bf16_out.is_cuda
+            self.last_stream_stats = streamer.step(
+                sc, pc, params, gc, grads, g_on_host, sc_, exp_avg, exp_avg_sq, n, bf16_out,
+                out_on_host, clip_coef, _stream_handle(stream, device))
 
     # ------------------------------------------------------------------
     # steps (layer_adam.py:270-468)

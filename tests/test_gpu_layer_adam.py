@@ -150,3 +150,68 @@ def test_errors(hip_device):
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a.cpu(), a, a)
     with pytest.raises(RuntimeError, match="size mismatch"):
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a[:5], a, a)
+
+
+# ---------------------------------------------------------------------------
+# host-state streaming (native chunk pipeline)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("chunk,slots,pinned,g_host,out_host", [
+    (1024, 2, True, False, False),     # many chunks, slot reuse, device grads + device bf16 copy
+    (4096, 3, True, True, True),       # the runtime's layout: grads and copy on the host
+    (16 * 1024 + 16, 1, False, True, False),  # pageable host memory, a single slot
+])
+def test_pipeline_matches_oracle(chunk, slots, pinned, g_host, out_host, hip_device):
+    from slideformer_amd.layer_adam import HostStreamer
+    print(f"pipeline chunk={chunk} slots={slots} pinned={pinned} g_host={g_host} out_host={out_host}", flush=True)
+    n = 100_003
+    rng = np.random.default_rng(chunk + slots)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32))
+    m = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32))
+    v = torch.from_numpy(np.abs(rng.normal(0, 1e-6, n)).astype(np.float32))
+    if pinned:
+        p, m, v = p.pin_memory(), m.pin_memory(), v.pin_memory()
+    ph, mh, vh = p.numpy().copy(), m.numpy().copy(), v.numpy().copy()
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=chunk, slots=slots)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    out = torch.empty(n, dtype=torch.bfloat16, device="cpu" if out_host else hip_device)
+    for step in (1, 2, 3):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        gd = g if g_host else g.to(hip_device)
+        adam.step_chunk(p, gd, m, v, dict(adam.defaults, step=step), bf16_out=out)
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16")
+        st = adam.last_stream_stats
+        assert st.chunks == -(-n // (chunk // 16 * 16))
+        assert st.h2d_bytes == n * (12 + (2 if g_host else 0))
+        assert st.d2h_bytes == n * (12 + (2 if out_host else 0))
+    torch.cuda.synchronize()
+    assert np.array_equal(p.numpy().view(np.uint32), ph.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(ph))
+
+
+def test_pipeline_with_clip_and_odd_tail(hip_device):
+    """Host state, device grads with a device clip coefficient; n with a scalar
+    tail in the last chunk only."""
+    from slideformer_amd.layer_adam import HostStreamer
+    n = 3 * 2048 + 13
+    rng = np.random.default_rng(77)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).pin_memory()
+    m = torch.zeros(n).pin_memory()
+    v = torch.zeros(n).pin_memory()
+    ph, mh, vh = p.numpy().copy(), m.numpy().copy(), v.numpy().copy()
+    adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=2048, slots=2)
+    g = torch.from_numpy(rng.normal(0, 1e-1, n).astype(np.float32)).bfloat16()
+    gd = g.to(hip_device)
+    coef, _ = adam.clip_grad_norm([gd], 1.0)
+    adam.step_chunk(p, gd, m, v, dict(adam.defaults, step=1), clip_coef=coef)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    orc.update(1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16",
+               clip_coef=float(coef.item()))
+    assert float(coef.item()) < 1.0
+    assert np.array_equal(p.numpy().view(np.uint32), ph.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
