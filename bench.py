@@ -227,6 +227,106 @@ def streamed(args):
     print(json.dumps(res), flush=True)
 
 
+QWEN14B_LAYER = [5120 * 5120, 5120, 5120 * 1024, 1024, 5120 * 1024, 1024, 5120 * 5120, 5120 * 13824,
+                 5120 * 13824, 13824 * 5120, 5120, 5120]  # q(+b), k(+b), v(+b), o, gate, up, down, 2 RMSNorm
+
+
+def resident_stack(args):
+    """Configs C3 (whole Llama-3.1-8B-shaped model) and C4 (48-layer
+    Qwen2.5-14B-shaped stack) with every layer's state resident in HBM, stepped
+    the way the runtime does it: layers registered with add_layer_params, grads
+    arriving in sliding order (last layer first, offload_transformer.py:265-301),
+    a global grad norm accumulated layer by layer, one clip coefficient, then
+    begin_chunk_step / step_chunk(bf16_out=...) / end_chunk_step per layer."""
+    import torch
+
+    from slideformer_amd import LayerAdam
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.config == "c3":
+        vocab = 128256
+        sizes = [vocab * 4096] + [sum(LLAMA8B_LAYER)] * 32 + [4096 + vocab * 4096]
+        lr, wd, gstd, outliers = 1e-5, 0.01, 1e-3, False
+        workload = ("C3 resident: Llama-3.1-8B-shaped model, embed + 32 decoder layers + norm/lm_head "
+                    "(8,030,261,248 params), all fp32 state in HBM, sliding order, global clip 1.0, bf16 copies")
+    else:
+        sizes = [sum(QWEN14B_LAYER)] * 48
+        lr, wd, gstd, outliers = 1e-5, 0.1, 1e-3, True
+        workload = ("C4: 48 Qwen2.5-14B-shaped layers (275,268,608 params each, 13,212,893,184 total), all "
+                    "state in HBM, bf16 grads N(0,1e-3) with 0.1% x100 outliers, AdamW wd 0.1, global clip 1.0")
+    n_total = sum(sizes)
+    log(f"resident {args.config}: {len(sizes)} layers, {n_total} params")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(60)
+    adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+    params, grads, outs = [], [], []
+    for idx, n in enumerate(sizes):
+        p = torch.randn(n, generator=gen, device=dev) * 0.02
+        g = (torch.randn(n, generator=gen, device=dev) * gstd).bfloat16()
+        if outliers:
+            sel = torch.randint(0, n, (n // 1000,), generator=gen, device=dev)
+            g[sel] = g[sel] * 100
+        params.append(p)
+        grads.append(g)
+        outs.append(torch.empty(n, dtype=torch.bfloat16, device=dev))
+        assert adam.add_layer_params(idx, [torch.nn.Parameter(p)]) == idx
+    torch.cuda.synchronize()
+    log(f"allocated {torch.cuda.memory_allocated(dev) / 2**30:.1f} GiB")
+    stream = torch.cuda.current_stream(dev)
+    order = list(range(len(sizes) - 1, -1, -1))  # sliding order: last layer's grads first
+
+    def one_step(evs=None):
+        acc = adam.grad_norm_begin(dev)
+        for idx in order:
+            acc.add(grads[idx], stream=stream)
+        coef, _ = acc.finish(1.0, stream=stream)
+        for j, idx in enumerate(order):
+            group = adam.begin_chunk_step(idx)
+            if evs is not None:
+                evs[j][0].record(stream)
+            adam.step_chunk(params[idx], grads[idx], adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], group,
+                            bf16_out=outs[idx], clip_coef=coef, stream=stream)
+            if evs is not None:
+                evs[j][1].record(stream)
+            adam.end_chunk_step(idx)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+           for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.steps):
+        one_step(evs[i])
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    upd = sum(a.elapsed_time(b) for step_evs in evs for a, b in step_evs) / args.steps
+    achieved = BYTES_PER_PARAM_UPDATE * n_total / (upd * 1e-3) / 1e9
+    res = {
+        "metric": f"LayerAdam full-model step, resident in HBM ({args.config}), Gparams/s",
+        "value": round(n_total / (ms * 1e-3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": workload, "params": n_total, "layers": len(sizes)},
+        "hbm_gbs_step": round(30 * n_total / (ms * 1e-3) / 1e9, 1),
+        "update_ms_per_step": round(upd, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "la_adamw_kernel<float, bf16_t, float> (all layers of a step)"},
+        "hbm_allocated_gib": round(torch.cuda.memory_allocated(dev) / 2**30, 1),
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +340,9 @@ def main():
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--streamed", choices=["c5", "c3"], default=None,
                     help="instead of C2: stream host-resident state through HBM (prints its own JSON line)")
+    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
+                    help="c2 (default, the headline): one Llama-3.1-8B layer; c3 / c4: whole resident "
+                         "model / 48-layer stack (prints its own JSON line)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -257,6 +360,9 @@ def main():
         sys.exit(1)
     if args.streamed:
         streamed(args)
+        return
+    if args.config != "c2":
+        resident_stack(args)
         return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

@@ -572,3 +572,57 @@ class LayerAdam:
                                                     float(max_norm), _ptr(coef), _ptr(norm), handle)
                 _lib.check(rc, "la_grad_sqnorm")
         return coef, norm
+
+    def grad_norm_begin(self, device=None) -> "GradNormAccumulator":
+        """Start a global grad norm over buffers that become ready one at a time.
+
+        In the runtime's sliding order (post-backward hooks, offload_transformer.py:265-301)
+        the last layer's grads exist long before the first layer's.  Call
+        ``acc.add(grad_flat)`` as each layer's grads land (asynchronous, on the
+        given stream), then ``coef, norm = acc.finish(max_norm)`` once every
+        buffer was added, and pass ``coef`` to each layer's ``step_chunk``."""
+        device = torch.device(device) if device is not None else (
+            self.device or torch.device('cuda', torch.cuda.current_device()))
+        return GradNormAccumulator(device)
+
+
+class GradNormAccumulator:
+    """Float64 sum of squares accumulated over several device buffers
+    (la_grad_sqnorm with accumulate), then one clip coefficient (la_clip_coef)."""
+
+    def __init__(self, device):
+        self.lib = _lib.load()
+        self.device = torch.device(device)
+        self.sqnorm = torch.zeros(1, dtype=torch.float64, device=self.device)
+        self.work = torch.empty(0, dtype=torch.float64, device=self.device)
+        self.count = 0
+
+    @torch.no_grad()
+    def add(self, grad: torch.Tensor, *, stream=None) -> None:
+        if grad.device != self.device:
+            raise RuntimeError(f"grad on {grad.device}, accumulator on {self.device}")
+        if not grad.is_contiguous():
+            raise RuntimeError("grads must be contiguous")
+        if grad.dtype not in _DTYPE_CODE:
+            raise RuntimeError(f"unsupported grad dtype {grad.dtype}")
+        need = max(1, self.lib.la_grad_sqnorm_workspace(grad.numel()) // 8)
+        if self.work.numel() < need:
+            self.work = torch.empty(need, dtype=torch.float64, device=self.device)
+        with torch.cuda.device(self.device):
+            _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[grad.dtype], _ptr(grad), grad.numel(),
+                                               _ptr(self.work), self.work.numel() * 8, _ptr(self.sqnorm),
+                                               int(self.count > 0), _stream_handle(stream, self.device)),
+                       "la_grad_sqnorm")
+        self.count += 1
+
+    @torch.no_grad()
+    def finish(self, max_norm: float, *, stream=None):
+        """``(coef, norm)`` as fp32 device scalars; no host synchronisation."""
+        coef = torch.empty(1, dtype=torch.float32, device=self.device)
+        norm = torch.empty(1, dtype=torch.float32, device=self.device)
+        with torch.cuda.device(self.device):
+            handle = _stream_handle(stream, self.device)
+            # with nothing added, sqnorm is still the zero it was created as: coef = 1
+            _lib.check(self.lib.la_clip_coef(_ptr(self.sqnorm), float(max_norm), _ptr(coef), _ptr(norm),
+                                             handle), "la_clip_coef")
+        return coef, norm

@@ -215,3 +215,96 @@ def test_pipeline_with_clip_and_odd_tail(hip_device):
     assert np.array_equal(p.numpy().view(np.uint32), ph.view(np.uint32))
     assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
     assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
+
+
+def test_global_norm_in_sliding_order(hip_device):
+    """Per-layer grads added one at a time (last layer first), one coefficient:
+    equal to the oracle's norm over all buffers."""
+    rng = np.random.default_rng(21)
+    sizes = [7, 4096 + 3, 100_000, 1]
+    grads = [torch.from_numpy(rng.normal(0, 1e-2, k).astype(np.float32)).bfloat16() for k in sizes]
+    adam = LayerAdam()
+    acc = adam.grad_norm_begin(hip_device)
+    for g in reversed(grads):
+        acc.add(g.to(hip_device))
+    coef, norm = acc.finish(1.0)
+    sq = sum(O.grad_sqnorm(H.to_np_bits(g, "bf16"), "bf16") for g in grads)
+    assert abs(acc.sqnorm.item() - sq) <= 1e-12 * sq
+    c_ref, n_ref = O.clip_coef(acc.sqnorm.item(), 1.0)
+    assert coef.item() == np.float32(c_ref) and norm.item() == np.float32(n_ref)
+    empty = adam.grad_norm_begin(hip_device)
+    c0, n0 = empty.finish(1.0)
+    assert c0.item() == 1.0 and n0.item() == 0.0
+
+
+def test_runtime_chunk_protocol_with_update_thread(hip_device):
+    """The runtime's protocol (transformer_layer.py:343-422, 453-493) on device
+    tensors: a producer publishes (cs, ce, event) per 32 Mi-element-style chunk
+    (here 4096) into a queue, an update thread waits on each event and calls
+    step_chunk on its own stream, writing the bf16 copy into a cache-unit
+    buffer; update_finished is set at the end.  Bit-exact with the oracle."""
+    import queue
+    import threading
+
+    n, chunk = 3 * 4096 + 5, 4096
+    rng = np.random.default_rng(31)
+    p_h = rng.normal(0, 0.02, n).astype(np.float32)
+    m_h = np.zeros(n, np.float32)
+    v_h = np.zeros(n, np.float32)
+    adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+    p = torch.from_numpy(p_h.copy()).to(hip_device)
+    adam.add_layer_params(0, [torch.nn.Parameter(p)])
+    cache_unit = torch.zeros(n, dtype=torch.bfloat16, device=hip_device)
+    produce = torch.cuda.Stream(device=hip_device)
+    update_stream = torch.cuda.Stream(device=hip_device)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        g32 = rng.normal(0, 1e-3, n).astype(np.float32)
+        grad = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+        q: "queue.Queue" = queue.Queue()
+        finished = threading.Event()
+        errors = []
+
+        def update_thread():
+            try:
+                group = adam.begin_chunk_step(0)
+                while True:
+                    item = q.get()
+                    if item is None:
+                        break
+                    cs, ce, ev = item
+                    update_stream.wait_event(ev)
+                    adam.step_chunk(p[cs:ce], grad[cs:ce], adam.exp_avg_flat[0][cs:ce],
+                                    adam.exp_avg_sq_flat[0][cs:ce], group, bf16_out=cache_unit[cs:ce],
+                                    stream=update_stream)
+                adam.end_chunk_step(0)
+                update_stream.synchronize()
+            except Exception as exc:  # surfaced to the main thread like Future.result()
+                errors.append(exc)
+            finally:
+                finished.set()
+
+        t = threading.Thread(target=update_thread)
+        t.start()
+        g_src = torch.from_numpy(g32).bfloat16()
+        with torch.cuda.stream(produce):
+            for cs in range(0, n, chunk):
+                ce = min(cs + chunk, n)
+                grad[cs:ce].copy_(g_src[cs:ce].to(hip_device, non_blocking=False))
+                ev = torch.cuda.Event()
+                ev.record(produce)
+                q.put((cs, ce, ev))
+        q.put(None)
+        finished.wait(timeout=60)
+        t.join(timeout=60)
+        assert not errors, errors
+        g_bits = H.to_np_bits(g_src, "bf16")
+        for cs in range(0, n, chunk):
+            ce = min(cs + chunk, n)
+            orc.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p_h[cs:ce], g_bits[cs:ce], m_h[cs:ce],
+                       v_h[cs:ce], g16="bf16")
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p, "f32"), p_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(adam.exp_avg_flat[0], "f32"), m_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(adam.exp_avg_sq_flat[0], "f32"), v_h.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(cache_unit, "bf16"), O.f32_to_bf16(p_h))
