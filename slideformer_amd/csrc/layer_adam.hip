@@ -68,6 +68,11 @@
 #ifndef LA_NT_STORE
 #define LA_NT_STORE 1
 #endif
+// Runs of 64 groups (256 elements) each wave of the update kernel handles per trip.
+#ifndef LA_IPL
+#define LA_IPL 1
+#endif
+static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
 
 namespace {
 
@@ -267,22 +272,39 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
 
-    for (uint64_t gi = tid; gi < a.nvec; gi += stride) {
-        const uint64_t e = a.head + gi * kVec;
-        float p[kVec], g[kVec], m[kVec], v[kVec];
-        Io<TG>::load4(a.g, e, g);
-        Io<TP>::load4(a.p, e, p);
-        Io<TS>::load4(a.m, e, m);
-        Io<TS>::load4(a.v, e, v);
+    // A wave owns LA_IPL runs of 64 groups (256 elements each); group j of lane
+    // L in wave w is w*64*LA_IPL + j*64 + L, so each wave instruction stays
+    // lane-contiguous.
+    const uint64_t lane = threadIdx.x & 63;
+    const uint64_t nwaves = stride >> 6;
+    for (uint64_t w = tid >> 6; w * 64 * LA_IPL < a.nvec; w += nwaves) {
+        float p[LA_IPL][kVec], g[LA_IPL][kVec], m[LA_IPL][kVec], v[LA_IPL][kVec];
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-            const float gj = has_coef ? g[j] * coef : g[j];
-            adam_body(p[j], gj, m[j], v[j], a.k);
+        for (int u = 0; u < LA_IPL; ++u) {
+            const uint64_t gi = (w * LA_IPL + u) * 64 + lane;
+            if (gi < a.nvec) {
+                const uint64_t e = a.head + gi * kVec;
+                Io<TG>::load4(a.g, e, g[u]);
+                Io<TP>::load4(a.p, e, p[u]);
+                Io<TS>::load4(a.m, e, m[u]);
+                Io<TS>::load4(a.v, e, v[u]);
+            }
         }
-        Io<TP>::store4(a.p, e, p);
-        Io<TS>::store4(a.m, e, m);
-        Io<TS>::store4(a.v, e, v);
-        if (a.out) Io<bf16_t>::store4(a.out, e, p);
+#pragma unroll
+        for (int u = 0; u < LA_IPL; ++u) {
+            const uint64_t gi = (w * LA_IPL + u) * 64 + lane;
+            if (gi >= a.nvec) continue;
+            const uint64_t e = a.head + gi * kVec;
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                const float gj = has_coef ? g[u][j] * coef : g[u][j];
+                adam_body(p[u][j], gj, m[u][j], v[u][j], a.k);
+            }
+            Io<TP>::store4(a.p, e, p[u]);
+            Io<TS>::store4(a.m, e, m[u]);
+            Io<TS>::store4(a.v, e, v[u]);
+            if (a.out) Io<bf16_t>::store4(a.out, e, p[u]);
+        }
     }
 
     // Elements outside the aligned groups: [0, head) and [head + 4*nvec, n).
@@ -492,7 +514,9 @@ template <typename TP, typename TG, typename TS>
 int launch_step(const StepArgs& a, hipStream_t stream)
 {
     const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-    const uint64_t work = a.nvec > nscalar ? a.nvec : nscalar;
+    // lanes needed: every wave takes LA_IPL runs of 64 groups
+    const uint64_t vec_lanes = (a.nvec + 64 * LA_IPL - 1) / (64 * LA_IPL) * 64;
+    const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
     hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK), 0, stream,
                        a);
     return hip_rc(hipGetLastError());
