@@ -9,6 +9,8 @@ north_star allows is 1e-6); NaN compared as a class.
 """
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -161,7 +163,7 @@ def test_every_triple_and_mode(triple, mode, hip_device):
     wd = 0.0 if mode == "none" else 0.05
     adamw = mode != "l2"
     bc = mode != "no_bc"
-    rng = np.random.default_rng(abs(hash((triple, mode))) % (2**31))
+    rng = np.random.default_rng(zlib.crc32(repr((triple, mode)).encode()))
     sizes = (100_003, 4096, 13)
     n = sum(sizes)
     p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(H.TD[pk])
@@ -385,3 +387,34 @@ def test_c4_qwen14b_layer_outliers(hip_device):
     n = sum(qwen14b_layer_sizes())
     assert n == 275_268_608
     _full_size_step(n, hip_device, warm_steps=0, wd=0.1, seed=30, outliers=True)
+
+
+def test_single_call_beyond_2_pow_31_elements(hip_device):
+    """64-bit indexing: one call over n = 2^31 + 2^20 + 13 elements (34 GB of HBM).
+    Elements are independent given the call's scalars, so windows at the start,
+    across the 2^31 boundary and at the end (holding the scalar tail) are
+    checked against the oracle, each window as its own one-call step."""
+    n = (1 << 31) + (1 << 20) + 13
+    log(f"n={n}")
+    gen = torch.Generator(device=hip_device)
+    gen.manual_seed(99)
+    p = torch.randn(n, generator=gen, device=hip_device) * 0.02
+    g = (torch.randn(n, generator=gen, device=hip_device) * 1e-3).bfloat16()
+    m = torch.zeros(n, device=hip_device)
+    v = torch.zeros(n, device=hip_device)
+    windows = [(0, 1 << 16), ((1 << 31) - (1 << 15), (1 << 31) + (1 << 15)), (n - (1 << 16) - 13, n)]
+    before = [(p[a:b].cpu().numpy().copy(), H.to_np_bits(g[a:b], "bf16")) for a, b in windows]
+    opt = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    opt.update(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v)
+    torch.cuda.synchronize()
+    for (a, b), (ph, gh) in zip(windows, before):
+        assert (b - a) % 16 == (n % 16 if b == n else 0)
+        mh = np.zeros(b - a, np.float32)
+        vh = np.zeros(b - a, np.float32)
+        orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+        orc.update(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, gh, mh, vh, g16="bf16")
+        assert np.array_equal(H.to_np_bits(p[a:b], "f32"), ph.view(np.uint32)), (a, b)
+        assert np.array_equal(H.to_np_bits(m[a:b], "f32"), mh.view(np.uint32)), (a, b)
+        assert np.array_equal(H.to_np_bits(v[a:b], "f32"), vh.view(np.uint32)), (a, b)
+    del p, g, m, v
+    torch.cuda.empty_cache()

@@ -12,6 +12,7 @@
 from __future__ import annotations
 
 import math
+import zlib
 
 import numpy as np
 import pytest
@@ -104,7 +105,7 @@ def test_oracle_matches_compiled_reference(triple, mode):
     pk, gk, sk = triple
     wd = 0.0 if mode == "none" else 0.05
     adamw = mode != "l2"
-    rng = np.random.default_rng(hash((triple, mode)) & 0xffff)
+    rng = np.random.default_rng(zlib.crc32(repr((triple, mode)).encode()))
     sizes = (100003, 16, 7)
     n = sum(sizes)
     p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(TD[pk])
