@@ -276,3 +276,34 @@ def test_clip_coef_matches_torch_clip_grad_norm():
         torch.testing.assert_close(torch.from_numpy(g.numpy() * np.float32(coef)), expected,
                                    rtol=2e-7, atol=0)
         torch.testing.assert_close(w.grad, expected, rtol=2e-7, atol=0)
+
+
+GPT2_SIZES = [768, 768, 768 * 2304, 2304, 768 * 768, 768, 768, 768, 768 * 3072, 3072, 3072 * 768, 768]
+
+
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_c1_gpt2_block_full_size_vs_compiled_reference(per_tensor):
+    """Config C1 on the CPU: the GPT-2-small block (7,087,872 params), 10 steps,
+    lr 1e-5, wd 0.01, fresh grads per step (seed 1000 + step), as one flat
+    step_chunk call or as one call per tensor (step / step_with_grad_views,
+    layer_adam.py:299-327).  Oracle == compiled reference, bit for bit."""
+    ref = _ref_or_skip()
+    n = sum(GPT2_SIZES)
+    assert n == 7_087_872
+    p0 = np.random.default_rng(1).normal(0, 0.02, n).astype(np.float32)
+    p = torch.from_numpy(p0.copy())
+    m, v = torch.zeros(n), torch.zeros(n)
+    pb, mb, vb = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    ref.create_adam(0, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
+    opt = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    bounds = np.cumsum([0] + GPT2_SIZES) if per_tensor else np.array([0, n])
+    for step in range(1, 11):
+        g = torch.from_numpy(np.random.default_rng(1000 + step).normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        gb = _np_bits(g, "bf16")
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            ref.adam_update(0, step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p[lo:hi], g[lo:hi], m[lo:hi], v[lo:hi])
+            opt.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, pb[lo:hi], gb[lo:hi], mb[lo:hi], vb[lo:hi],
+                       g16="bf16")
+    assert np.array_equal(p.numpy().view(np.uint32), pb.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), mb.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), vb.view(np.uint32))
