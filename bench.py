@@ -327,6 +327,48 @@ def resident_stack(args):
     print(json.dumps(res), flush=True)
 
 
+def disk_bench(args):
+    """The NVMe moment offload (LayerAdam(nvme_offload_fraction=1.0)) on this
+    host: write and read back one C2 layer's exp_avg + exp_avg_sq (2 x 872 MB)
+    through the native offloader, as _offload_layer / _load_layer do."""
+    import torch
+
+    from slideformer_amd.nvme import DiskOffloader
+
+    n = sum(LLAMA8B_LAYER)
+    os.makedirs(args.disk_bench, exist_ok=True)
+    off = DiskOffloader(args.disk_bench, 16, 'uring')
+    m = torch.randn(n)
+    v = torch.rand(n)
+    m_ref, v_ref = m.clone(), v.clone()
+    nbytes = 2 * n * 4
+    w, r = [], []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        off.async_write(m)
+        off.async_write(v)
+        off.sync_write_events()
+        t1 = time.perf_counter()
+        off.async_read(m)
+        off.async_read(v)
+        off.sync_read_events()
+        t2 = time.perf_counter()
+        w.append(t1 - t0)
+        r.append(t2 - t1)
+    assert torch.equal(m, m_ref) and torch.equal(v, v_ref)
+    res = {
+        "metric": "LayerAdam moment file offload (write, read back), GB/s",
+        "value": round(nbytes / (sum(r) / len(r)) / 1e9, 2),
+        "unit": "GB/s (read)",
+        "write_gbs": round(nbytes / (sum(w) / len(w)) / 1e9, 2),
+        "bytes_per_layer": nbytes,
+        "steps": args.steps,
+        "dir": args.disk_bench,
+        "note": "buffered positioned I/O on 16 worker threads; the page cache may hold the data",
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,6 +382,8 @@ def main():
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--streamed", choices=["c5", "c3"], default=None,
                     help="instead of C2: stream host-resident state through HBM (prints its own JSON line)")
+    ap.add_argument("--disk-bench", default=None, metavar="DIR",
+                    help="instead of C2: time the moment file offload into DIR (host only)")
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
                     help="c2 (default, the headline): one Llama-3.1-8B layer; c3 / c4: whole resident "
                          "model / 48-layer stack (prints its own JSON line)")
@@ -350,6 +394,10 @@ def main():
               "(the LayerAdam step is elementwise and would shard by contiguous slices; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.disk_bench:
+        disk_bench(args)
+        return
 
     import torch
 

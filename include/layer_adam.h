@@ -176,6 +176,28 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
                      const float* clip_coef, void* workspace, uint64_t workspace_bytes,
                      la_stream_t after, int synchronize, la_pipeline_stats_t* stats);
 
+/*
+ * Asynchronous file offload of host state buffers (the NVMe moment offload).
+ * Replaces tensornvme's DiskOffloader as LayerAdam uses it
+ * (layer_adam.py:92-106 construction, :200-247 async_read / async_write /
+ * sync_read_events / sync_write_events).  A pool of `threads` workers does
+ * positioned reads/writes in 64 MiB pieces; one file per key,
+ * "<dir>/offload-<pid>-<key>", removed by la_disk_destroy.
+ *   la_disk_write_async / la_disk_read_async: queue the transfer of `bytes`
+ *     from / into host memory that must stay valid until the matching sync.
+ *     A read of a key never written returns -ENOENT.
+ *   la_disk_sync_writes / la_disk_sync_reads: wait for every queued write /
+ *     read; return 0 or the first failure as a negative errno.
+ */
+typedef struct la_disk la_disk_t;
+
+int la_disk_create(const char* dir, int threads, la_disk_t** out);
+int la_disk_destroy(la_disk_t* d);
+int la_disk_write_async(la_disk_t* d, uint64_t key, const void* src, uint64_t bytes);
+int la_disk_read_async(la_disk_t* d, uint64_t key, void* dst, uint64_t bytes);
+int la_disk_sync_writes(la_disk_t* d);
+int la_disk_sync_reads(la_disk_t* d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,12 @@ EXPORTED = (
     "la_pipeline_create",
     "la_pipeline_destroy",
     "la_pipeline_step",
+    "la_disk_create",
+    "la_disk_destroy",
+    "la_disk_write_async",
+    "la_disk_read_async",
+    "la_disk_sync_writes",
+    "la_disk_sync_reads",
 )
 
 
@@ -116,6 +122,18 @@ def _declare(L):
     L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, i, P, P, u64, P, i, P, P, u64, P, i,
                                    ctypes.POINTER(LaPipelineStats)]
     L.la_pipeline_step.restype = i
+    L.la_disk_create.argtypes = [ctypes.c_char_p, i, ctypes.POINTER(P)]
+    L.la_disk_create.restype = i
+    L.la_disk_destroy.argtypes = [P]
+    L.la_disk_destroy.restype = i
+    L.la_disk_write_async.argtypes = [P, u64, P, u64]
+    L.la_disk_write_async.restype = i
+    L.la_disk_read_async.argtypes = [P, u64, P, u64]
+    L.la_disk_read_async.restype = i
+    L.la_disk_sync_writes.argtypes = [P]
+    L.la_disk_sync_writes.restype = i
+    L.la_disk_sync_reads.argtypes = [P]
+    L.la_disk_sync_reads.restype = i
     return L
 
 

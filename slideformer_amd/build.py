@@ -22,7 +22,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libslideformer_amd.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
-SOURCES = [os.path.join(CSRC, "layer_adam.hip"), os.path.join(CSRC, "pipeline.hip")]
+SOURCES = [os.path.join(CSRC, "layer_adam.hip"), os.path.join(CSRC, "pipeline.hip"),
+           os.path.join(CSRC, "disk_offload.hip")]
 ARCH = "gfx950"
 
 BASE_FLAGS = [

@@ -211,11 +211,9 @@ class LayerAdam:
         self.last_stream_stats = None
 
         if self.nvme_offload_fraction > 0.0:
-            # layer_adam.py:92-101; the NVMe state offload is not part of this build.
-            try:
-                from tensornvme import DiskOffloader
-            except ModuleNotFoundError:
-                raise ModuleNotFoundError("Please install tensornvme to use NVMeOptimizer")
+            # layer_adam.py:92-101: same construction, with the native file
+            # offloader of this package in place of tensornvme's
+            from .nvme import DiskOffloader
             assert offload_dir is not None, "offload_dir cannot be None"
             self.offload_dir = offload_dir
             self.offloader = DiskOffloader(self.offload_dir, 16, 'uring')
@@ -260,6 +258,9 @@ class LayerAdam:
         layer_numel = sum(p.numel() for p in params)
         state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
         device = params[0].device
+        if self.offloader is not None and device.type != 'cpu':
+            # as in the reference, the file offload moves host-resident moments
+            raise RuntimeError("nvme_offload_fraction > 0 needs host-resident params and state")
         self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
         self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
         offset = 0

@@ -1,0 +1,107 @@
+"""File offload of LayerAdam's host moment buffers (the NVMe path).
+
+``DiskOffloader`` has the interface of tensornvme's class as the reference's
+LayerAdam uses it (layer_adam.py:92-106 construction, :200-247 use):
+``async_write(t)`` queues the buffer's bytes to its file and, once
+``sync_write_events()`` has seen the write land, releases the tensor's
+storage; ``async_read(t)`` re-allocates the storage and queues the read,
+complete after ``sync_read_events()``.  Views into the buffer (LayerAdam's
+per-parameter ``state`` views) stay valid across the release/re-allocation
+because they share the storage object.  The I/O runs on the native worker
+pool of ``libslideformer_amd.so`` (``la_disk_*``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Dict, List
+
+import torch
+
+from . import _lib
+
+
+class DiskOffloader:
+    def __init__(self, dir_name: str, n_entries: int = 16, backend: str = 'uring'):
+        # `backend` names tensornvme's I/O engine; here every backend is the
+        # native thread pool, `n_entries` bounds its size.
+        self.lib = _lib.load()
+        self.dir_name = os.path.abspath(dir_name)
+        os.makedirs(self.dir_name, exist_ok=True)
+        self.backend = backend
+        handle = ctypes.c_void_p()
+        rc = self.lib.la_disk_create(self.dir_name.encode(), max(1, min(int(n_entries), 16)),
+                                     ctypes.byref(handle))
+        if rc != 0:
+            raise OSError(-rc, f"la_disk_create({self.dir_name}) failed: {os.strerror(-rc) if rc < 0 else rc}")
+        self.handle = handle
+        self._nbytes: Dict[int, int] = {}
+        self._pending_writes: List[torch.Tensor] = []
+        self._pending_reads: List[torch.Tensor] = []
+
+    @staticmethod
+    def _check_tensor(t: torch.Tensor):
+        if t.device.type != 'cpu':
+            raise RuntimeError("DiskOffloader moves host tensors only")
+        if not t.is_contiguous() or t.storage_offset() != 0:
+            raise RuntimeError("DiskOffloader needs a whole contiguous buffer")
+
+    def _io_error(self, rc: int, what: str):
+        if rc != 0:
+            raise OSError(-rc if rc < 0 else rc, f"{what} failed: {os.strerror(-rc) if rc < 0 else rc}")
+
+    def async_write(self, tensor: torch.Tensor) -> None:
+        self._check_tensor(tensor)
+        nbytes = tensor.numel() * tensor.element_size()
+        if tensor.untyped_storage().nbytes() < nbytes:
+            raise RuntimeError("async_write of a buffer whose storage was already released")
+        self._nbytes[id(tensor)] = nbytes
+        self._io_error(self.lib.la_disk_write_async(self.handle, id(tensor), tensor.data_ptr(), nbytes),
+                       "la_disk_write_async")
+        self._pending_writes.append(tensor)
+
+    def async_read(self, tensor: torch.Tensor) -> None:
+        """Bring the buffer back.  A buffer whose storage was never released
+        (never written, or written but not yet fenced by sync_write_events)
+        still holds the current bytes, so nothing is read; a pending release
+        of it is cancelled."""
+        self._check_tensor(tensor)
+        if any(tensor is w for w in self._pending_writes):
+            self._pending_writes = [w for w in self._pending_writes if w is not tensor]
+            return
+        nbytes = self._nbytes.get(id(tensor))
+        storage = tensor.untyped_storage()
+        if nbytes is None or storage.nbytes() >= nbytes:
+            return
+        storage.resize_(nbytes)
+        self._io_error(self.lib.la_disk_read_async(self.handle, id(tensor), tensor.data_ptr(), nbytes),
+                       "la_disk_read_async")
+        self._pending_reads.append(tensor)
+
+    def sync_write_events(self) -> None:
+        rc = self.lib.la_disk_sync_writes(self.handle)
+        written, self._pending_writes = self._pending_writes, []
+        self._io_error(rc, "la_disk_sync_writes")
+        for t in written:
+            t.untyped_storage().resize_(0)  # the bytes live in the file now
+
+    def sync_read_events(self) -> None:
+        rc = self.lib.la_disk_sync_reads(self.handle)
+        self._pending_reads = []
+        self._io_error(rc, "la_disk_sync_reads")
+
+    def sync_write(self, tensor: torch.Tensor) -> None:
+        self.async_write(tensor)
+        self.sync_write_events()
+
+    def sync_read(self, tensor: torch.Tensor) -> None:
+        self.async_read(tensor)
+        self.sync_read_events()
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                self.lib.la_disk_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass

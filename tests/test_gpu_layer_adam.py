@@ -308,3 +308,46 @@ def test_runtime_chunk_protocol_with_update_thread(hip_device):
     assert np.array_equal(H.to_np_bits(adam.exp_avg_flat[0], "f32"), m_h.view(np.uint32))
     assert np.array_equal(H.to_np_bits(adam.exp_avg_sq_flat[0], "f32"), v_h.view(np.uint32))
     assert np.array_equal(H.to_np_bits(cache_unit, "bf16"), O.f32_to_bf16(p_h))
+
+
+@pytest.mark.parametrize("fraction,prefetch", [(1.0, True), (0.3, False)])
+def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path):
+    """Host state with the moments offloaded to files between layer steps
+    (layer_adam.py:92-106, 200-247): layers stepped last-to-first for two
+    iterations with the runtime's chunk calls; prefetch loads layer i-1 while
+    layer i is stepped.  Bit-exact with the oracle."""
+    sizes = [5000, 4096 + 7, 300, 10_001]
+    L_ = len(sizes)
+    rng = np.random.default_rng(int(fraction * 10) + prefetch)
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, num_layer=L_, nvme_offload_fraction=fraction,
+                     offload_dir=str(tmp_path), prefetch=prefetch)
+    p_host = [rng.normal(0, 0.02, k).astype(np.float32) for k in sizes]
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in p_host]
+    for i, p in enumerate(params):
+        adam.add_layer_params(i, [p])
+    m_h = [np.zeros(k, np.float32) for k in sizes]
+    v_h = [np.zeros(k, np.float32) for k in sizes]
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for it in range(2):
+        for idx in range(L_ - 1, -1, -1):
+            g = torch.from_numpy(rng.normal(0, 1e-3, sizes[idx]).astype(np.float32)).bfloat16()
+            group = adam.begin_chunk_step(idx)
+            if not prefetch:
+                adam.offloader.sync_read_events()
+            assert adam.exp_avg_flat[idx].untyped_storage().nbytes() == sizes[idx] * 4
+            adam.step_chunk(params[idx].data, g.to(hip_device), adam.exp_avg_flat[idx],
+                            adam.exp_avg_sq_flat[idx], group)
+            adam.end_chunk_step(idx)
+            orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p_host[idx], H.to_np_bits(g, "bf16"),
+                       m_h[idx], v_h[idx], g16="bf16")
+    adam.offloader.sync_write_events()
+    for idx in range(L_):
+        assert np.array_equal(params[idx].data.numpy().view(np.uint32), p_host[idx].view(np.uint32))
+        adam._load_layer(idx)
+        adam.offloader.sync_read_events()
+        assert np.array_equal(adam.exp_avg_flat[idx].numpy().view(np.uint32), m_h[idx].view(np.uint32))
+        if fraction > 0.5:
+            assert np.array_equal(adam.exp_avg_sq_flat[idx].numpy().view(np.uint32), v_h[idx].view(np.uint32))
+        else:
+            assert adam.exp_avg_sq_flat[idx].untyped_storage().nbytes() == sizes[idx] * 4
+            assert np.array_equal(adam.exp_avg_sq_flat[idx].numpy().view(np.uint32), v_h[idx].view(np.uint32))
