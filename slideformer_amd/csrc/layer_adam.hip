@@ -68,10 +68,6 @@
 #ifndef LA_NT_STORE
 #define LA_NT_STORE 1
 #endif
-// Runs of 64 groups (256 elements) each wave of the update kernel handles per trip.
-#ifndef LA_IPL
-#define LA_IPL 1
-#endif
 static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
 
 namespace {
@@ -209,6 +205,60 @@ struct ConvF16 {
 template <> struct Io<bf16_t> : Io16<ConvBf16> {};
 template <> struct Io<f16_t> : Io16<ConvF16> {};
 
+// Raw buffer access for the update kernel: 4 consecutive elements per lane at
+// byte offset lane * 4 * sizeof(T) from a per-wave descriptor.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kRsrcFlags = 0x00020000;          // word 3 of a gfx9 raw buffer descriptor
+constexpr int kAux = (LA_NT_LOAD ? 2 : 0);      // cache-policy bits: nt
+constexpr int kAuxSt = (LA_NT_STORE ? 2 : 0);
+
+template <typename T> struct WaveIo;
+
+template <> struct WaveIo<float> {
+    __device__ __forceinline__ static rsrc_t rsrc(const void* base, uint64_t e0, uint32_t nel)
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(static_cast<const float*>(base) + e0), 0,
+                                                 static_cast<int>(nel * 4), kRsrcFlags);
+    }
+    __device__ __forceinline__ static void load4(rsrc_t r, uint32_t lane, float (&x)[kVec])
+    {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(lane * 16), 0, kAux);
+        x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y);
+        x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+    }
+    __device__ __forceinline__ static void store4(rsrc_t r, uint32_t lane, const float (&x)[kVec])
+    {
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(x[0]), __float_as_uint(x[1]),
+                                                     __float_as_uint(x[2]), __float_as_uint(x[3])},
+                                               r, static_cast<int>(lane * 16), 0, kAuxSt);
+    }
+};
+
+template <typename Conv> struct WaveIo16 {
+    __device__ __forceinline__ static rsrc_t rsrc(const void* base, uint64_t e0, uint32_t nel)
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(static_cast<const uint16_t*>(base) + e0), 0,
+                                                 static_cast<int>(nel * 2), kRsrcFlags);
+    }
+    __device__ __forceinline__ static void load4(rsrc_t r, uint32_t lane, float (&x)[kVec])
+    {
+        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(lane * 8), 0, kAux);
+        x[0] = Conv::to_f32(u.x & 0xffffu);
+        x[1] = Conv::to_f32(u.x >> 16);
+        x[2] = Conv::to_f32(u.y & 0xffffu);
+        x[3] = Conv::to_f32(u.y >> 16);
+    }
+    __device__ __forceinline__ static void store4(rsrc_t r, uint32_t lane, const float (&x)[kVec])
+    {
+        const uint32_t lo = Conv::from_f32(x[0]) | (Conv::from_f32(x[1]) << 16);
+        const uint32_t hi = Conv::from_f32(x[2]) | (Conv::from_f32(x[3]) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, r, static_cast<int>(lane * 8), 0, kAuxSt);
+    }
+};
+template <> struct WaveIo<bf16_t> : WaveIo16<ConvBf16> {};
+template <> struct WaveIo<f16_t> : WaveIo16<ConvF16> {};
+
 // ---------------------------------------------------------------------------
 // the element update
 // ---------------------------------------------------------------------------
@@ -272,39 +322,36 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
 
-    // A wave owns LA_IPL runs of 64 groups (256 elements each); group j of lane
-    // L in wave w is w*64*LA_IPL + j*64 + L, so each wave instruction stays
-    // lane-contiguous.
-    const uint64_t lane = threadIdx.x & 63;
+    // Wave w owns groups [64w, 64w + 64): one lane-contiguous run of 256
+    // elements per stream.  Each stream is addressed through a raw buffer
+    // descriptor whose base is the wave's first element (scalar registers) and
+    // whose size covers only the wave's valid groups, so the lanes of a partial
+    // last wave need no branch: their loads return 0 and their stores are
+    // dropped by the hardware range check.
+    const uint32_t lane = threadIdx.x & 63;
     const uint64_t nwaves = stride >> 6;
-    for (uint64_t w = tid >> 6; w * 64 * LA_IPL < a.nvec; w += nwaves) {
-        float p[LA_IPL][kVec], g[LA_IPL][kVec], m[LA_IPL][kVec], v[LA_IPL][kVec];
+    for (uint64_t w = tid >> 6; w * 64 < a.nvec; w += nwaves) {
+        const uint64_t left = a.nvec - w * 64;
+        const uint32_t nel = (left < 64 ? static_cast<uint32_t>(left) : 64u) * kVec;
+        const uint64_t e0 = a.head + w * 64 * kVec;
+        const rsrc_t rg = WaveIo<TG>::rsrc(a.g, e0, nel);
+        const rsrc_t rp = WaveIo<TP>::rsrc(a.p, e0, nel);
+        const rsrc_t rm = WaveIo<TS>::rsrc(a.m, e0, nel);
+        const rsrc_t rv = WaveIo<TS>::rsrc(a.v, e0, nel);
+        float p[kVec], g[kVec], m[kVec], v[kVec];
+        WaveIo<TG>::load4(rg, lane, g);
+        WaveIo<TP>::load4(rp, lane, p);
+        WaveIo<TS>::load4(rm, lane, m);
+        WaveIo<TS>::load4(rv, lane, v);
 #pragma unroll
-        for (int u = 0; u < LA_IPL; ++u) {
-            const uint64_t gi = (w * LA_IPL + u) * 64 + lane;
-            if (gi < a.nvec) {
-                const uint64_t e = a.head + gi * kVec;
-                Io<TG>::load4(a.g, e, g[u]);
-                Io<TP>::load4(a.p, e, p[u]);
-                Io<TS>::load4(a.m, e, m[u]);
-                Io<TS>::load4(a.v, e, v[u]);
-            }
+        for (int j = 0; j < kVec; ++j) {
+            const float gj = has_coef ? g[j] * coef : g[j];
+            adam_body(p[j], gj, m[j], v[j], a.k);
         }
-#pragma unroll
-        for (int u = 0; u < LA_IPL; ++u) {
-            const uint64_t gi = (w * LA_IPL + u) * 64 + lane;
-            if (gi >= a.nvec) continue;
-            const uint64_t e = a.head + gi * kVec;
-#pragma unroll
-            for (int j = 0; j < kVec; ++j) {
-                const float gj = has_coef ? g[u][j] * coef : g[u][j];
-                adam_body(p[u][j], gj, m[u][j], v[u][j], a.k);
-            }
-            Io<TP>::store4(a.p, e, p[u]);
-            Io<TS>::store4(a.m, e, m[u]);
-            Io<TS>::store4(a.v, e, v[u]);
-            if (a.out) Io<bf16_t>::store4(a.out, e, p[u]);
-        }
+        WaveIo<TP>::store4(rp, lane, p);
+        WaveIo<TS>::store4(rm, lane, m);
+        WaveIo<TS>::store4(rv, lane, v);
+        if (a.out) WaveIo<bf16_t>::store4(WaveIo<bf16_t>::rsrc(a.out, e0, nel), lane, p);
     }
 
     // Elements outside the aligned groups: [0, head) and [head + 4*nvec, n).
@@ -514,8 +561,8 @@ template <typename TP, typename TG, typename TS>
 int launch_step(const StepArgs& a, hipStream_t stream)
 {
     const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-    // lanes needed: every wave takes LA_IPL runs of 64 groups
-    const uint64_t vec_lanes = (a.nvec + 64 * LA_IPL - 1) / (64 * LA_IPL) * 64;
+    // lanes needed: every wave takes one run of 64 groups
+    const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
     const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
     hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK), 0, stream,
                        a);
