@@ -14,7 +14,8 @@ import threading
 
 import torch  # noqa: F401  (binds the HIP runtime before the library is loaded)
 
-from .build import LIB_PATH
+# where slideformer_amd/build.py writes the library
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libslideformer_amd.so")
 
 LA_OK = 0
 LA_EINVAL = -22

@@ -152,8 +152,18 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     if (p_dtype < LA_F32 || p_dtype > LA_F16 || g_dtype < LA_F32 || g_dtype > LA_F16 || s_dtype < LA_F32 ||
         s_dtype > LA_F16)
         return LA_EDTYPE;
+    // the dtype triple is checked up front (an n = 0 call validates without launching),
+    // so a bad triple cannot stop the chunk loop half-way
+    {
+        const int rc = la_adamw_step(sc, p_dtype, nullptr, g_dtype, nullptr, s_dtype, nullptr, nullptr, 0, nullptr,
+                                     nullptr, nullptr);
+        if (rc != LA_OK) return rc;
+    }
     if (n == 0) return LA_OK;
     if (!p_host || !g || !m_host || !v_host || !workspace) return LA_EINVAL;
+    if (!g_on_host && reinterpret_cast<uintptr_t>(g) % static_cast<uintptr_t>(esize(g_dtype))) return LA_EINVAL;
+    if (out && !out_on_host && (reinterpret_cast<uintptr_t>(out) & 1u)) return LA_EINVAL;
+    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
     if (out_on_host && !out) return LA_EINVAL;
     if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return LA_EINVAL;
     const SlotLayout L = slot_layout(pl->chunk, p_dtype, g_dtype, s_dtype, g_on_host, out_on_host && out);

@@ -351,3 +351,44 @@ def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path)
         else:
             assert adam.exp_avg_sq_flat[idx].untyped_storage().nbytes() == sizes[idx] * 4
             assert np.array_equal(adam.exp_avg_sq_flat[idx].numpy().view(np.uint32), v_h[idx].view(np.uint32))
+
+
+def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
+    """la_pipeline_step validates the dtype triple and device-pointer alignment
+    up front: the host state is left untouched."""
+    import ctypes
+
+    from slideformer_amd import _lib
+    from slideformer_amd.layer_adam import HostStreamer
+
+    L = _lib.load()
+    s = HostStreamer(hip_device, chunk_elems=1024, slots=2)
+    n = 4096
+    p = torch.randn(n).pin_memory()
+    m = torch.zeros(n).pin_memory()
+    v = torch.zeros(n).pin_memory()
+    p_before = p.clone()
+    g = torch.zeros(n + 1, dtype=torch.bfloat16, device=hip_device)
+    L.la_create(77, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0)
+    sc = _lib.LaScalars()
+    assert L.la_scalars(77, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.byref(sc)) == 0
+    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, False, False)
+    base = (ws.data_ptr() + 255) // 256 * 256
+    st = torch.cuda.current_stream(hip_device).cuda_stream
+    # (f32, bf16, bf16) is not a registered triple
+    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
+                            _lib.LA_BF16, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, ws.numel() - 256, st,
+                            1, None)
+    assert rc == _lib.LA_EDTYPE
+    # a device grad pointer at an odd byte address
+    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr() + 1,
+                            0, _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, ws.numel() - 256,
+                            st, 1, None)
+    assert rc == _lib.LA_EINVAL
+    # too small a workspace
+    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
+                            _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, 1024, st, 1, None)
+    assert rc == _lib.LA_EINVAL
+    torch.cuda.synchronize()
+    assert torch.equal(p, p_before) and not m.any() and not v.any()
+    L.la_destroy(77)
