@@ -133,18 +133,18 @@ def streamed(args):
     if args.streamed == "c5":
         n, chunk, slots, lr, gstd = sum(C5_LAYER), 64 * 1024 * 1024, 2, 6e-6, 5e-4
         workload = ("C5: one 100B-class dense layer (hidden 12288, FFN 49152, biases), 1,812,099,072 params; "
-                    "fp32 p/m/v in pinned host RAM, 256 MB double-buffered chunks; bf16 grads and bf16 copy in HBM")
+                    "fp32 p/m/v in host RAM, 256 MB double-buffered chunks; bf16 grads and bf16 copy in HBM")
     else:
         n, chunk, slots, lr, gstd = sum(LLAMA8B_LAYER), 16 * 1024 * 1024, 3, 1e-5, 1e-3
         workload = ("C3 layer: one Llama-3.1-8B-shaped layer (218,112,000 params) of the streamed model; "
-                    "fp32 p/m/v in pinned host RAM, 64 MB chunks x 3 slots; bf16 grads and bf16 copy in HBM")
+                    "fp32 p/m/v in host RAM, 64 MB chunks x 3 slots; bf16 grads and bf16 copy in HBM")
     assert n % 16 == 0
     log(f"streamed {args.streamed}: n={n}, chunk={chunk}, slots={slots}")
     gen = torch.Generator(device=dev)
     gen.manual_seed(50)
     host = []
     for std in (0.02, 0.0, 0.0):
-        t = torch.empty(n, dtype=torch.float32, pin_memory=True)
+        t = torch.empty(n, dtype=torch.float32, pin_memory=not args.pageable)
         piece = 256 * 1024 * 1024
         for lo in range(0, n, piece):
             hi = min(n, lo + piece)
@@ -155,7 +155,7 @@ def streamed(args):
     g = (torch.randn(n, generator=gen, device=dev) * gstd).bfloat16()
     out = torch.empty(n, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
-    log("pinned state allocated and initialised")
+    log(("pageable" if args.pageable else "pinned") + " state allocated and initialised")
 
     adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
     adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots)
@@ -214,7 +214,8 @@ def streamed(args):
         "higher_is_better": True,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots},
+        "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots,
+                   "host_memory": "pageable" if args.pageable else "pinned"},
         "h2d_gbs_effective": round(h2d_bytes / (wall * 1e-3) / 1e9, 2),
         "d2h_gbs_effective": round(d2h_bytes / (wall * 1e-3) / 1e9, 2),
         "h2d_gbs_isolated": round(h2d_bytes / (t_h2d * 1e-3) / 1e9, 2),
@@ -380,6 +381,8 @@ def main():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, run one torch fp32 copy_ of this many MiB: a plain copy "
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
+    ap.add_argument("--pageable", action="store_true",
+                    help="with --streamed: host state in pageable instead of pinned memory")
     ap.add_argument("--streamed", choices=["c5", "c3"], default=None,
                     help="instead of C2: stream host-resident state through HBM (prints its own JSON line)")
     ap.add_argument("--disk-bench", default=None, metavar="DIR",

@@ -111,6 +111,7 @@ class HostStreamer:
         except Exception:
             pass
 
+
 _ids = itertools.count()
 _ids_lock = threading.Lock()
 
@@ -175,7 +176,12 @@ class LayerAdam:
             prefetch: bool = True,
             *,
             device: Optional[torch.device] = None,
+            pin_host_state: bool = False,
     ):
+        """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
+        ``device``: the HIP device that updates host-resident state (default: current);
+        ``pin_host_state``: allocate host-resident moments in page-locked memory
+        (faster streaming; the reference allocates pageable memory)."""
         self.defaults = dict(
             lr=lr,
             bias_correction=bias_correction,
@@ -199,6 +205,7 @@ class LayerAdam:
         self.fp32_optimizer_state = fp32_optimizer_state
         self.num_layer = num_layer
         self.device = torch.device(device) if device is not None else None
+        self.pin_host_state = pin_host_state
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
         assert 0.0 <= nvme_offload_fraction <= 1.0
@@ -251,6 +258,10 @@ class LayerAdam:
         params = list(params)
         if not params:
             return -1
+        device = params[0].device
+        if self.offloader is not None and device.type != 'cpu':
+            # as in the reference, the file offload moves host-resident moments
+            raise RuntimeError("nvme_offload_fraction > 0 needs host-resident params and state")
         param_group = {
             'params': params,
             'layer_idx': layer_idx,
@@ -260,12 +271,14 @@ class LayerAdam:
         self.param_groups.append(param_group)
         layer_numel = sum(p.numel() for p in params)
         state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
-        device = params[0].device
-        if self.offloader is not None and device.type != 'cpu':
-            # as in the reference, the file offload moves host-resident moments
-            raise RuntimeError("nvme_offload_fraction > 0 needs host-resident params and state")
-        self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
-        self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
+        # host moments are page-locked on request: the streaming pipeline then
+        # moves them at the host link's DMA rate instead of through bounce buffers
+        # (not with the file offload, which releases and re-allocates these buffers)
+        pin = (device.type == 'cpu' and self.pin_host_state and self.offloader is None
+               and torch.cuda.is_available())
+        self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device, pin_memory=pin)
+        self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device,
+                                                      pin_memory=pin)
         offset = 0
         for p in params:
             size = p.numel()

@@ -353,6 +353,27 @@ def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path)
             assert np.array_equal(adam.exp_avg_sq_flat[idx].numpy().view(np.uint32), v_h[idx].view(np.uint32))
 
 
+def test_pinned_host_state_layer_step(hip_device):
+    """pin_host_state=True: add_layer_params allocates page-locked host moments;
+    step(layer) on host params streams them; bit-exact with the oracle."""
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, pin_host_state=True)
+    rng = np.random.default_rng(41)
+    x = rng.normal(0, 0.02, 50_003).astype(np.float32)
+    p = torch.nn.Parameter(torch.from_numpy(x.copy()))
+    adam.add_layer_params(0, [p])
+    assert adam.exp_avg_flat[0].is_pinned() and adam.exp_avg_sq_flat[0].is_pinned()
+    m_h, v_h = np.zeros_like(x), np.zeros_like(x)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        g = rng.normal(0, 1e-3, x.size).astype(np.float32)
+        p.grad = torch.from_numpy(g.copy())
+        adam.step(0)
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, x, g, m_h, v_h)
+    assert np.array_equal(p.data.numpy().view(np.uint32), x.view(np.uint32))
+    assert np.array_equal(adam.exp_avg_flat[0].numpy().view(np.uint32), m_h.view(np.uint32))
+    assert np.array_equal(adam.exp_avg_sq_flat[0].numpy().view(np.uint32), v_h.view(np.uint32))
+
+
 def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     """la_pipeline_step validates the dtype triple and device-pointer alignment
     up front: the host state is left untouched."""
