@@ -117,10 +117,13 @@ C5_LAYER = [12288 * 3 * 12288, 3 * 12288, 12288 * 12288, 12288, 12288 * 49152, 4
 
 
 def streamed(args):
-    """Configs C5 (one 100B-class dense layer) / C3-shaped layers with fp32 state in
-    pinned host RAM, streamed through HBM by the native chunk pipeline.  Reports
-    the streamed step rate, the effective H2D/D2H GB/s, the isolated rates of
-    each stage and the overlap (sum of isolated times / wall)."""
+    """Configs C5 (one 100B-class dense layer) / one C3-shaped layer with fp32
+    state in host RAM (pinned; pageable with --pageable), streamed through HBM by
+    the native chunk pipeline.  Reports the streamed step rate, the effective
+    H2D/D2H GB/s, the isolated rates of each stage and the overlap (sum of
+    isolated times / wall).  With --pageable the isolated copies are torch
+    copy_ calls on the same pageable arrays, i.e. the HIP runtime's own
+    bounce-buffer path that the pipeline's staging replaces."""
     import ctypes
 
     import torch
@@ -130,6 +133,9 @@ def streamed(args):
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.streamed == "c3":
+        streamed_model(args)
+        return
     if args.streamed == "c5":
         n, chunk, slots, lr, gstd = sum(C5_LAYER), 64 * 1024 * 1024, 2, 6e-6, 5e-4
         workload = ("C5: one 100B-class dense layer (hidden 12288, FFN 49152, biases), 1,812,099,072 params; "
@@ -158,8 +164,9 @@ def streamed(args):
     log(("pageable" if args.pageable else "pinned") + " state allocated and initialised")
 
     adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
-    adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots)
-    walls = []
+    adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads,
+                                        stage_pageable=not args.no_staging)
+    walls, host_copy = [], []
     t = 0
     for i in range(args.warmup + args.steps):
         t += 1
@@ -167,6 +174,7 @@ def streamed(args):
         st = adam.last_stream_stats
         if i >= args.warmup:
             walls.append(st.wall_ms)
+            host_copy.append(st.host_copy_ms)
     wall = sum(walls) / len(walls)
     h2d_bytes, d2h_bytes = st.h2d_bytes, st.d2h_bytes
 
@@ -215,7 +223,11 @@ def streamed(args):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots,
-                   "host_memory": "pageable" if args.pageable else "pinned"},
+                   "host_memory": "pageable" if args.pageable else "pinned",
+                   "pageable_copies": ("none" if not args.pageable else
+                                       "HIP runtime bounce buffers" if args.no_staging else
+                                       f"page-locked slot twins, host threads {args.host_threads or 'default'}")},
+        "host_copy_ms": round(sum(host_copy) / len(host_copy), 3),
         "h2d_gbs_effective": round(h2d_bytes / (wall * 1e-3) / 1e9, 2),
         "d2h_gbs_effective": round(d2h_bytes / (wall * 1e-3) / 1e9, 2),
         "h2d_gbs_isolated": round(h2d_bytes / (t_h2d * 1e-3) / 1e9, 2),
@@ -224,6 +236,116 @@ def streamed(args):
         "overlap": round((t_h2d + t_d2h + t_comp) / wall, 3),
         "stream_spans_ms": {"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
                             "d2h": round(st.d2h_ms, 3)},
+    }
+    print(json.dumps(res), flush=True)
+
+
+def llama8b_model_sizes():
+    """Flat buffer sizes of the Llama-3.1-8B-shaped model in layer-index order:
+    embed, 32 decoder layers, final norm + lm_head (8,030,261,248 params)."""
+    vocab = 128256
+    return [vocab * 4096] + [sum(LLAMA8B_LAYER)] * 32 + [4096 + vocab * 4096]
+
+
+def streamed_model(args):
+    """Config C3: the whole Llama-3.1-8B-shaped model with every layer's fp32
+    master, m and v in host RAM, bf16 grads and bf16 copies in HBM.  The state
+    is allocated as the reference allocates it, in pageable memory
+    (transformer_layer.py:192-196, layer_adam.py:161-173); 96 GB is also more
+    than the GPU hosts here let one process page-lock.  The pipeline copies it
+    through page-locked twins of its slots with native host threads.  One step =
+    a global grad norm accumulated in sliding order, one clip coefficient, then
+    each layer streamed through HBM in 64 MB chunks (16 Mi fp32 elements, 3
+    slots), in sliding order (lm_head, L31 ... L0, embed;
+    offload_transformer.py:265-301)."""
+    import torch
+
+    from slideformer_amd import LayerAdam
+    from slideformer_amd.layer_adam import HostStreamer
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    sizes = llama8b_model_sizes()
+    n_total = sum(sizes)
+    chunk, slots = 16 * 1024 * 1024, 3
+    log(f"streamed c3 model: {len(sizes)} layers, {n_total} params, chunk={chunk}, slots={slots}")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(70)
+    adam = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads)
+    params, grads, outs = [], [], []
+    piece = 256 * 1024 * 1024
+    for idx, n in enumerate(sizes):
+        p = torch.empty(n, dtype=torch.float32)
+        for lo in range(0, n, piece):
+            hi = min(n, lo + piece)
+            p[lo:hi].copy_(torch.randn(hi - lo, generator=gen, device=dev) * 0.02)
+        params.append(p)
+        grads.append((torch.randn(n, generator=gen, device=dev) * 1e-3).bfloat16())
+        outs.append(torch.empty(n, dtype=torch.bfloat16, device=dev))
+        assert adam.add_layer_params(idx, [torch.nn.Parameter(p)]) == idx
+        if idx % 8 == 0 or idx == len(sizes) - 1:
+            log(f"layer {idx} allocated (host master + moments, {n} params)")
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    order = list(range(len(sizes) - 1, -1, -1))
+
+    def one_step():
+        t0 = time.perf_counter()
+        acc = adam.grad_norm_begin(dev)
+        for idx in order:
+            acc.add(grads[idx], stream=stream)
+        coef, _ = acc.finish(1.0, stream=stream)
+        spans = [0.0, 0.0, 0.0, 0.0]
+        for idx in order:
+            group = adam.begin_chunk_step(idx)
+            adam.step_chunk(params[idx], grads[idx], adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], group,
+                            bf16_out=outs[idx], clip_coef=coef, stream=stream)
+            st = adam.last_stream_stats
+            spans[0] += st.h2d_ms
+            spans[1] += st.compute_ms
+            spans[2] += st.d2h_ms
+            spans[3] += st.host_copy_ms
+            adam.end_chunk_step(idx)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, spans
+
+    for i in range(args.warmup):
+        one_step()
+        log(f"warm-up step {i + 1} done")
+    walls, span_sum = [], [0.0, 0.0, 0.0, 0.0]
+    for i in range(args.steps):
+        w, spans = one_step()
+        walls.append(w)
+        span_sum = [a + b for a, b in zip(span_sum, spans)]
+        log(f"step {i + 1}: {w:.3f} s")
+    wall = sum(walls) / len(walls)
+    each_way = 12 * n_total
+    res = {
+        "metric": "streamed LayerAdam full-model step (host-resident fp32 state), Gparams/s",
+        "value": round(n_total / wall / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 1),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": ("C3: Llama-3.1-8B-shaped model, embed + 32 decoder layers + norm/lm_head "
+                                "(8,030,261,248 params); fp32 p/m/v in pageable host RAM (the reference's "
+                                "allocation), staged through page-locked slot twins by native host threads, "
+                                "streamed in 64 MB chunks x 3 slots in sliding order; global clip 1.0; bf16 "
+                                "grads and copies in HBM"),
+                   "params": n_total, "layers": len(sizes), "chunk_elems": chunk, "slots": slots},
+        "h2d_gbs_effective": round(each_way / wall / 1e9, 2),
+        "d2h_gbs_effective": round(each_way / wall / 1e9, 2),
+        "bytes_each_way_per_step": each_way,
+        "stream_spans_ms_per_step": {k: round(s / len(walls), 1) for k, s in zip(("h2d", "update", "d2h"),
+                                                                                  span_sum)},
+        "host_copy_ms_per_step": round(span_sum[3] / len(walls), 1),
+        "host_threads": adam._streamers[dev].host_threads or "default (up to 16)",
+        "wall_clock": "host perf_counter around the whole step (norm, clip, every layer's streamed update)",
     }
     print(json.dumps(res), flush=True)
 
@@ -246,8 +368,7 @@ def resident_stack(args):
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.config == "c3":
-        vocab = 128256
-        sizes = [vocab * 4096] + [sum(LLAMA8B_LAYER)] * 32 + [4096 + vocab * 4096]
+        sizes = llama8b_model_sizes()
         lr, wd, gstd, outliers = 1e-5, 0.01, 1e-3, False
         workload = ("C3 resident: Llama-3.1-8B-shaped model, embed + 32 decoder layers + norm/lm_head "
                     "(8,030,261,248 params), all fp32 state in HBM, sliding order, global clip 1.0, bf16 copies")
@@ -383,8 +504,13 @@ def main():
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--pageable", action="store_true",
                     help="with --streamed: host state in pageable instead of pinned memory")
-    ap.add_argument("--streamed", choices=["c5", "c3"], default=None,
-                    help="instead of C2: stream host-resident state through HBM (prints its own JSON line)")
+    ap.add_argument("--host-threads", type=int, default=0,
+                    help="with --streamed: host threads that stage pageable arrays (0 = up to 16)")
+    ap.add_argument("--no-staging", action="store_true",
+                    help="with --streamed --pageable: leave pageable arrays to the HIP runtime's bounce buffers")
+    ap.add_argument("--streamed", choices=["c5", "c3", "c3-layer"], default=None,
+                    help="instead of C2: stream host-resident state through HBM (prints its own JSON line); "
+                         "c3 = the whole model, c3-layer = one of its decoder layers")
     ap.add_argument("--disk-bench", default=None, metavar="DIR",
                     help="instead of C2: time the moment file offload into DIR (host only)")
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 1
+#define LA_ABI_VERSION 2
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -153,23 +153,36 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   before the call runs first; work queued on `after` later sees the
  *   result.  synchronize != 0 (or stats != NULL) waits for completion.
  *   One pipeline object must not be used by two threads at once.
+ * la_pipeline_set_host_staging: attach caller-owned page-locked host memory
+ *   (256-byte aligned, at least la_pipeline_workspace_bytes() for the call's
+ *   types and placements) and the number of host copy threads (0 = up to 16),
+ *   or detach it with pinned = NULL.  While attached, la_pipeline_step copies
+ *   every pageable host array through it: `threads` host threads copy each
+ *   chunk into the page-locked twin of its slot and the results back out, and
+ *   the copy engines only ever see page-locked memory.  Without it pageable
+ *   arrays go through the HIP runtime's own bounce buffers.  A call that
+ *   stages returns after completion whatever `synchronize` says.  No
+ *   reference counterpart: the reference updates pageable state on the CPU.
  */
 typedef struct la_pipeline la_pipeline_t;
 
 typedef struct {
-    float wall_ms;      /* first H2D start .. last D2H end */
+    float wall_ms;      /* first H2D start .. last D2H end; with staging, the whole call (host clock) */
     float h2d_ms;       /* span of the H2D stream (includes waits for free slots) */
     float compute_ms;   /* span of the compute stream */
     float d2h_ms;       /* span of the D2H stream */
     uint64_t h2d_bytes;
     uint64_t d2h_bytes;
     uint32_t chunks;
+    float host_copy_ms;     /* time the host threads spent copying through the staging */
+    uint64_t staged_bytes;  /* bytes they copied (both directions) */
 } la_pipeline_stats_t;
 
 uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtype, int g_dtype,
                                      int s_dtype, int g_on_host, int out_on_host);
 int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out);
 int la_pipeline_destroy(la_pipeline_t* pl);
+int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads);
 int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host,
                      int g_dtype, const void* g, int g_on_host, int s_dtype, void* m_host,
                      void* v_host, uint64_t n, uint16_t* out, int out_on_host,

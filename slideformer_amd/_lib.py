@@ -39,6 +39,7 @@ EXPORTED = (
     "la_pipeline_workspace_bytes",
     "la_pipeline_create",
     "la_pipeline_destroy",
+    "la_pipeline_set_host_staging",
     "la_pipeline_step",
     "la_disk_create",
     "la_disk_destroy",
@@ -60,6 +61,8 @@ class LaPipelineStats(ctypes.Structure):
         ("h2d_bytes", ctypes.c_uint64),
         ("d2h_bytes", ctypes.c_uint64),
         ("chunks", ctypes.c_uint32),
+        ("host_copy_ms", ctypes.c_float),
+        ("staged_bytes", ctypes.c_uint64),
     ]
 
 
@@ -120,6 +123,8 @@ def _declare(L):
     L.la_pipeline_create.restype = i
     L.la_pipeline_destroy.argtypes = [P]
     L.la_pipeline_destroy.restype = i
+    L.la_pipeline_set_host_staging.argtypes = [P, P, u64, i]
+    L.la_pipeline_set_host_staging.restype = i
     L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, i, P, P, u64, P, i, P, P, u64, P, i,
                                    ctypes.POINTER(LaPipelineStats)]
     L.la_pipeline_step.restype = i

@@ -15,15 +15,32 @@
 // stages, so copies in both directions overlap the update of other chunks.
 // Chunks are multiples of 16 elements, so only the last chunk of a call holds
 // the reference's scalar tail.  The caller owns the device staging memory.
+//
+// Pageable host arrays (the reference allocates its moments with plain
+// torch.zeros, layer_adam.py:161-173) cannot be reached by the copy engines
+// directly; the runtime would bounce them through small internal buffers at a
+// fraction of the link rate.  With page-locked host staging attached
+// (la_pipeline_set_host_staging), each slot gets a page-locked twin: a pool of
+// host threads copies chunk i of every pageable array into the twin, the copy
+// engines move the twin, and after the copy-back the threads copy the results
+// out of the twin before chunk i + S reuses it.
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <chrono>
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <new>
+#include <thread>
 #include <vector>
 
 #include "../../include/layer_adam.h"
+#include "copy_pool.h"
+
+using la_host::CopyPool;
+using la_host::Piece;
 
 struct la_pipeline {
     int device = 0;
@@ -33,6 +50,10 @@ struct la_pipeline {
     std::vector<hipEvent_t> ev_h2d, ev_comp, ev_d2h;
     hipEvent_t t_begin = nullptr, t_h2d_end = nullptr, t_comp_end = nullptr, t_end = nullptr, t_comp_begin = nullptr,
                t_d2h_begin = nullptr;
+    // page-locked host staging for pageable arrays (caller-owned; null = none)
+    char* host_staging = nullptr;
+    uint64_t host_staging_bytes = 0;
+    std::unique_ptr<CopyPool> pool;
 };
 
 namespace {
@@ -66,11 +87,39 @@ SlotLayout slot_layout(uint64_t chunk, int p_dt, int g_dt, int s_dt, int g_on_ho
 
 int rc_of(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
 
-#define LA_TRY(expr)                           \
-    do {                                       \
-        const hipError_t e_ = (expr);          \
-        if (e_ != hipSuccess) return rc_of(e_); \
-    } while (0)
+// Host memory the copy engines can read and write directly: page-locked
+// (hipHostMalloc, torch pin_memory) or registered.  Anything else is pageable.
+bool page_locked(const void* ptr)
+{
+    hipPointerAttribute_t a;
+    std::memset(&a, 0, sizeof(a));
+    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
+        (void)hipGetLastError();  // a query of pageable memory must not leave an error behind
+        return false;
+    }
+    return a.type == hipMemoryTypeHost;
+}
+
+// Host copies are split into pieces of at most this many bytes for the pool.
+constexpr uint64_t kPieceBytes = 1ull << 20;
+
+void add_pieces(std::vector<Piece>& out, void* dst, const void* src, uint64_t bytes)
+{
+    char* d = static_cast<char*>(dst);
+    const char* s = static_cast<const char*>(src);
+    for (uint64_t o = 0; o < bytes; o += kPieceBytes)
+        out.push_back(Piece{d + o, s + o, std::min(kPieceBytes, bytes - o)});
+}
+
+// After a failure part-way through a call, let the queued copies finish before
+// returning, so that nothing still writes the caller's memory afterwards.
+int drain_streams(la_pipeline* pl, int rc)
+{
+    (void)hipStreamSynchronize(pl->h2d);
+    (void)hipStreamSynchronize(pl->comp);
+    (void)hipStreamSynchronize(pl->d2h);
+    return rc;
+}
 
 void destroy_events(la_pipeline* pl)
 {
@@ -142,11 +191,37 @@ int la_pipeline_destroy(la_pipeline_t* pl)
     return LA_OK;
 }
 
+int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads)
+{
+    if (!pl) return LA_EINVAL;
+    if (!pinned) {
+        pl->host_staging = nullptr;
+        pl->host_staging_bytes = 0;
+        return LA_OK;
+    }
+    if (bytes == 0 || reinterpret_cast<uintptr_t>(pinned) % kAlign || threads < 0 || threads > 64) return LA_EINVAL;
+    char* base = static_cast<char*>(pinned);
+    if (!page_locked(base) || !page_locked(base + bytes - 1)) return LA_EINVAL;
+    if (threads == 0) threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
+    if (!pl->pool || pl->pool->threads() != threads) {
+        pl->pool.reset();
+        try {
+            pl->pool.reset(new CopyPool(threads));
+        } catch (...) {
+            return LA_EINVAL;
+        }
+    }
+    pl->host_staging = base;
+    pl->host_staging_bytes = bytes;
+    return LA_OK;
+}
+
 int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host, int g_dtype, const void* g,
                      int g_on_host, int s_dtype, void* m_host, void* v_host, uint64_t n, uint16_t* out,
                      int out_on_host, const float* clip_coef, void* workspace, uint64_t workspace_bytes,
                      la_stream_t after, int synchronize, la_pipeline_stats_t* stats)
 {
+    const auto t0 = std::chrono::steady_clock::now();
     if (stats) std::memset(stats, 0, sizeof(*stats));
     if (!pl || !sc) return LA_EINVAL;
     if (p_dtype < LA_F32 || p_dtype > LA_F16 || g_dtype < LA_F32 || g_dtype > LA_F16 || s_dtype < LA_F32 ||
@@ -167,7 +242,20 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     if (out_on_host && !out) return LA_EINVAL;
     if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return LA_EINVAL;
     const SlotLayout L = slot_layout(pl->chunk, p_dtype, g_dtype, s_dtype, g_on_host, out_on_host && out);
-    if (workspace_bytes < L.slot_bytes * static_cast<uint64_t>(pl->slots)) return LA_EINVAL;
+    const uint64_t ws_need = L.slot_bytes * static_cast<uint64_t>(pl->slots);
+    if (workspace_bytes < ws_need) return LA_EINVAL;
+
+    // which host arrays go through the page-locked staging (pageable ones, when it is attached)
+    bool st_p = false, st_m = false, st_v = false, st_g = false, st_o = false;
+    if (pl->host_staging) {
+        st_p = !page_locked(p_host);
+        st_m = !page_locked(m_host);
+        st_v = !page_locked(v_host);
+        st_g = g_on_host && !page_locked(g);
+        st_o = out && out_on_host && !page_locked(out);
+    }
+    const bool staged = st_p || st_m || st_v || st_g || st_o;
+    if (staged && pl->host_staging_bytes < ws_need) return LA_EINVAL;
 
     const int pb = esize(p_dtype), gb = esize(g_dtype), sb = esize(s_dtype);
     char* ws = static_cast<char*>(workspace);
@@ -177,62 +265,130 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     const char* gp = static_cast<const char*>(g);
     char* op = reinterpret_cast<char*>(out);
     const uint64_t nchunks = (n + pl->chunk - 1) / pl->chunk;
+    const uint64_t S = static_cast<uint64_t>(pl->slots);
     hipStream_t caller = static_cast<hipStream_t>(after);
-    uint64_t h2d_bytes = 0, d2h_bytes = 0;
+    uint64_t h2d_bytes = 0, d2h_bytes = 0, staged_bytes = 0;
+    double host_copy_ms = 0.0;
+    std::vector<Piece> pieces;
+
+    auto host_copy = [&]() {
+        const auto a = std::chrono::steady_clock::now();
+        pl->pool->run(pieces);
+        host_copy_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - a).count();
+        for (const Piece& q : pieces) staged_bytes += q.bytes;
+        pieces.clear();
+    };
+    // results of chunk j leave the page-locked twin of its slot (staged arrays only)
+    auto copy_out = [&](uint64_t j) -> int {
+        const uint64_t s = j % S, off = j * pl->chunk;
+        const uint64_t k = (n - off) < pl->chunk ? (n - off) : pl->chunk;
+        char* hs = pl->host_staging + s * L.slot_bytes;
+        const hipError_t e = hipEventSynchronize(pl->ev_d2h[s]);
+        if (e != hipSuccess) return rc_of(e);
+        if (st_p) add_pieces(pieces, ph + off * pb, hs + L.p, k * pb);
+        if (st_m) add_pieces(pieces, mh + off * sb, hs + L.m, k * sb);
+        if (st_v) add_pieces(pieces, vh + off * sb, hs + L.v, k * sb);
+        if (st_o) add_pieces(pieces, op + off * 2, hs + L.out, k * 2);
+        host_copy();
+        return LA_OK;
+    };
+
+#define LA_STEP_TRY(expr)                                         \
+    do {                                                          \
+        const hipError_t e_ = (expr);                             \
+        if (e_ != hipSuccess) return drain_streams(pl, rc_of(e_)); \
+    } while (0)
 
     // the slots are free once the previous call's last copy-back is done
-    LA_TRY(hipStreamWaitEvent(pl->h2d, pl->t_end, 0));
+    LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->t_end, 0));
     // everything the caller queued before (e.g. the backward that produced g) comes first
-    LA_TRY(hipEventRecord(pl->t_begin, caller));
-    LA_TRY(hipStreamWaitEvent(pl->h2d, pl->t_begin, 0));
-    LA_TRY(hipStreamWaitEvent(pl->comp, pl->t_begin, 0));
-    LA_TRY(hipStreamWaitEvent(pl->d2h, pl->t_begin, 0));
-    LA_TRY(hipEventRecord(pl->t_comp_begin, pl->comp));
-    LA_TRY(hipEventRecord(pl->t_d2h_begin, pl->d2h));
+    LA_STEP_TRY(hipEventRecord(pl->t_begin, caller));
+    LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->t_begin, 0));
+    LA_STEP_TRY(hipStreamWaitEvent(pl->comp, pl->t_begin, 0));
+    LA_STEP_TRY(hipStreamWaitEvent(pl->d2h, pl->t_begin, 0));
+    LA_STEP_TRY(hipEventRecord(pl->t_comp_begin, pl->comp));
+    LA_STEP_TRY(hipEventRecord(pl->t_d2h_begin, pl->d2h));
+    // host threads read the host arrays directly: the caller's queued work and the
+    // previous call's copy-backs must be complete before they do
+    if (staged) {
+        LA_STEP_TRY(hipEventSynchronize(pl->t_begin));
+        LA_STEP_TRY(hipStreamSynchronize(pl->d2h));
+    }
 
     for (uint64_t i = 0; i < nchunks; ++i) {
-        const int s = static_cast<int>(i % static_cast<uint64_t>(pl->slots));
+        const uint64_t s = i % S;
         const uint64_t off = i * pl->chunk;
         const uint64_t k = (n - off) < pl->chunk ? (n - off) : pl->chunk;
-        char* slot = ws + static_cast<uint64_t>(s) * L.slot_bytes;
-        if (i >= static_cast<uint64_t>(pl->slots)) LA_TRY(hipStreamWaitEvent(pl->h2d, pl->ev_d2h[s], 0));
-        LA_TRY(hipMemcpyAsync(slot + L.p, ph + off * pb, k * pb, hipMemcpyHostToDevice, pl->h2d));
-        LA_TRY(hipMemcpyAsync(slot + L.m, mh + off * sb, k * sb, hipMemcpyHostToDevice, pl->h2d));
-        LA_TRY(hipMemcpyAsync(slot + L.v, vh + off * sb, k * sb, hipMemcpyHostToDevice, pl->h2d));
+        char* slot = ws + s * L.slot_bytes;
+        char* hs = staged ? pl->host_staging + s * L.slot_bytes : nullptr;
+        if (staged) {
+            if (i >= S) {
+                const int rc = copy_out(i - S);
+                if (rc != LA_OK) return drain_streams(pl, rc);
+            }
+            if (st_p) add_pieces(pieces, hs + L.p, ph + off * pb, k * pb);
+            if (st_m) add_pieces(pieces, hs + L.m, mh + off * sb, k * sb);
+            if (st_v) add_pieces(pieces, hs + L.v, vh + off * sb, k * sb);
+            if (st_g) add_pieces(pieces, hs + L.g, gp + off * gb, k * gb);
+            host_copy();
+        }
+        if (i >= S) LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->ev_d2h[s], 0));
+        LA_STEP_TRY(hipMemcpyAsync(slot + L.p, st_p ? hs + L.p : ph + off * pb, k * pb, hipMemcpyHostToDevice,
+                                   pl->h2d));
+        LA_STEP_TRY(hipMemcpyAsync(slot + L.m, st_m ? hs + L.m : mh + off * sb, k * sb, hipMemcpyHostToDevice,
+                                   pl->h2d));
+        LA_STEP_TRY(hipMemcpyAsync(slot + L.v, st_v ? hs + L.v : vh + off * sb, k * sb, hipMemcpyHostToDevice,
+                                   pl->h2d));
         h2d_bytes += k * (pb + 2 * sb);
         const void* gdev = gp + off * gb;
         if (g_on_host) {
-            LA_TRY(hipMemcpyAsync(slot + L.g, gp + off * gb, k * gb, hipMemcpyHostToDevice, pl->h2d));
+            LA_STEP_TRY(hipMemcpyAsync(slot + L.g, st_g ? hs + L.g : gp + off * gb, k * gb, hipMemcpyHostToDevice,
+                                       pl->h2d));
             h2d_bytes += k * gb;
             gdev = slot + L.g;
         }
-        LA_TRY(hipEventRecord(pl->ev_h2d[s], pl->h2d));
+        LA_STEP_TRY(hipEventRecord(pl->ev_h2d[s], pl->h2d));
 
-        LA_TRY(hipStreamWaitEvent(pl->comp, pl->ev_h2d[s], 0));
+        LA_STEP_TRY(hipStreamWaitEvent(pl->comp, pl->ev_h2d[s], 0));
         uint16_t* odev = nullptr;
         if (out) odev = out_on_host ? reinterpret_cast<uint16_t*>(slot + L.out) : out + off;
         const int rc = la_adamw_step(sc, p_dtype, slot + L.p, g_dtype, gdev, s_dtype, slot + L.m, slot + L.v, k,
                                      odev, clip_coef, pl->comp);
-        if (rc != LA_OK) return rc;
-        LA_TRY(hipEventRecord(pl->ev_comp[s], pl->comp));
+        if (rc != LA_OK) return drain_streams(pl, rc);
+        LA_STEP_TRY(hipEventRecord(pl->ev_comp[s], pl->comp));
 
-        LA_TRY(hipStreamWaitEvent(pl->d2h, pl->ev_comp[s], 0));
-        LA_TRY(hipMemcpyAsync(ph + off * pb, slot + L.p, k * pb, hipMemcpyDeviceToHost, pl->d2h));
-        LA_TRY(hipMemcpyAsync(mh + off * sb, slot + L.m, k * sb, hipMemcpyDeviceToHost, pl->d2h));
-        LA_TRY(hipMemcpyAsync(vh + off * sb, slot + L.v, k * sb, hipMemcpyDeviceToHost, pl->d2h));
+        LA_STEP_TRY(hipStreamWaitEvent(pl->d2h, pl->ev_comp[s], 0));
+        LA_STEP_TRY(hipMemcpyAsync(st_p ? hs + L.p : ph + off * pb, slot + L.p, k * pb, hipMemcpyDeviceToHost,
+                                   pl->d2h));
+        LA_STEP_TRY(hipMemcpyAsync(st_m ? hs + L.m : mh + off * sb, slot + L.m, k * sb, hipMemcpyDeviceToHost,
+                                   pl->d2h));
+        LA_STEP_TRY(hipMemcpyAsync(st_v ? hs + L.v : vh + off * sb, slot + L.v, k * sb, hipMemcpyDeviceToHost,
+                                   pl->d2h));
         d2h_bytes += k * (pb + 2 * sb);
         if (out && out_on_host) {
-            LA_TRY(hipMemcpyAsync(op + off * 2, slot + L.out, k * 2, hipMemcpyDeviceToHost, pl->d2h));
+            LA_STEP_TRY(hipMemcpyAsync(st_o ? hs + L.out : op + off * 2, slot + L.out, k * 2, hipMemcpyDeviceToHost,
+                                       pl->d2h));
             d2h_bytes += k * 2;
         }
-        LA_TRY(hipEventRecord(pl->ev_d2h[s], pl->d2h));
+        LA_STEP_TRY(hipEventRecord(pl->ev_d2h[s], pl->d2h));
     }
-    LA_TRY(hipEventRecord(pl->t_h2d_end, pl->h2d));
-    LA_TRY(hipEventRecord(pl->t_comp_end, pl->comp));
-    LA_TRY(hipEventRecord(pl->t_end, pl->d2h));
+    LA_STEP_TRY(hipEventRecord(pl->t_h2d_end, pl->h2d));
+    LA_STEP_TRY(hipEventRecord(pl->t_comp_end, pl->comp));
+    LA_STEP_TRY(hipEventRecord(pl->t_end, pl->d2h));
     // later work on the caller's stream sees the updated state
-    LA_TRY(hipStreamWaitEvent(caller, pl->t_end, 0));
-    if (synchronize || stats) LA_TRY(hipEventSynchronize(pl->t_end));
+    LA_STEP_TRY(hipStreamWaitEvent(caller, pl->t_end, 0));
+    if (staged) {
+        // the last S chunks still sit in their page-locked twins
+        for (uint64_t j = nchunks > S ? nchunks - S : 0; j < nchunks; ++j) {
+            const int rc = copy_out(j);
+            if (rc != LA_OK) return drain_streams(pl, rc);
+        }
+    }
+#undef LA_STEP_TRY
+    if (synchronize || stats) {
+        const hipError_t e = hipEventSynchronize(pl->t_end);
+        if (e != hipSuccess) return rc_of(e);
+    }
     if (stats) {
         stats->h2d_bytes = h2d_bytes;
         stats->d2h_bytes = d2h_bytes;
@@ -241,6 +397,11 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
         (void)hipEventElapsedTime(&stats->h2d_ms, pl->t_begin, pl->t_h2d_end);
         (void)hipEventElapsedTime(&stats->compute_ms, pl->t_comp_begin, pl->t_comp_end);
         (void)hipEventElapsedTime(&stats->d2h_ms, pl->t_d2h_begin, pl->t_end);
+        stats->staged_bytes = staged_bytes;
+        stats->host_copy_ms = static_cast<float>(host_copy_ms);
+        if (staged)
+            stats->wall_ms = static_cast<float>(
+                std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count());
     }
     return LA_OK;
 }

@@ -14,7 +14,9 @@ Host tensors (the reference's layout: fp32 master and moments in CPU RAM) are
 streamed through HBM in 8 Mi-element chunks by the library's native
 three-stream pipeline (H2D / update / D2H overlapped) and the call returns
 after completion, as the reference's CPU call does; grads and the bf16 copy may
-then live on the host or on the device.  There is no CPU arithmetic path.
+then live on the host or on the device.  Pageable host arrays are copied
+through page-locked staging by native host threads.  There is no CPU
+arithmetic path.
 
 Additions, all keyword-only so that positional signatures are unchanged:
 ``bf16_out=`` (the bf16 compute copy written in the same pass), ``clip_coef=``
@@ -65,33 +67,63 @@ HOST_STAGE_SLOTS = 4
 
 class HostStreamer:
     """One native chunk pipeline (``la_pipeline_t``) on one device, plus the
-    device staging memory it needs (allocated here, never by the library)."""
+    device staging memory it needs (allocated here, never by the library).
 
-    def __init__(self, device, chunk_elems: int = HOST_STAGE_ELEMS, slots: int = HOST_STAGE_SLOTS):
+    Pageable host arrays (the reference's moments are plain ``torch.zeros``,
+    layer_adam.py:161-173) go through page-locked twins of the staging slots,
+    copied by ``host_threads`` native threads (0 = up to 16); the copy engines
+    then only see page-locked memory.  ``stage_pageable=False`` leaves pageable
+    arrays to the HIP runtime's own bounce buffers instead."""
+
+    def __init__(self, device, chunk_elems: int = HOST_STAGE_ELEMS, slots: int = HOST_STAGE_SLOTS, *,
+                 host_threads: int = 0, stage_pageable: bool = True):
         self.lib = _lib.load()
         self.device = torch.device(device)
         self.chunk = chunk_elems
         self.slots = slots
+        self.host_threads = host_threads
+        self.stage_pageable = stage_pageable
         handle = ctypes.c_void_p()
         with torch.cuda.device(self.device):
             _lib.check(self.lib.la_pipeline_create(chunk_elems, slots, ctypes.byref(handle)),
                        "la_pipeline_create")
         self.handle = handle
         self._ws = {}
+        self._host_ws = {}
+
+    def _bytes(self, key) -> int:
+        return self.lib.la_pipeline_workspace_bytes(self.chunk, self.slots, *[int(k) for k in key])
 
     def workspace(self, pc, gc, sc, g_on_host, out_on_host) -> torch.Tensor:
         key = (pc, gc, sc, g_on_host, out_on_host)
         ws = self._ws.get(key)
         if ws is None:
-            nbytes = self.lib.la_pipeline_workspace_bytes(self.chunk, self.slots, pc, gc, sc,
-                                                          int(g_on_host), int(out_on_host))
-            ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
+            ws = torch.empty(self._bytes(key) + 256, dtype=torch.uint8, device=self.device)
             self._ws[key] = ws
         return ws
 
+    def _attach_host_staging(self, key, needed: bool):
+        if not needed:
+            _lib.check(self.lib.la_pipeline_set_host_staging(self.handle, None, 0, 0),
+                       "la_pipeline_set_host_staging")
+            return
+        buf = self._host_ws.get(key)
+        if buf is None:
+            buf = torch.empty(self._bytes(key) + 256, dtype=torch.uint8, pin_memory=True)
+            self._host_ws[key] = buf
+        base = buf.data_ptr()
+        aligned = (base + 255) // 256 * 256
+        _lib.check(self.lib.la_pipeline_set_host_staging(self.handle, aligned, buf.numel() - (aligned - base),
+                                                         self.host_threads),
+                   "la_pipeline_set_host_staging")
+
     def step(self, scalars, pc, params, gc, grads, g_on_host, sc, exp_avg, exp_avg_sq, n, bf16_out,
              out_on_host, clip_coef, stream_handle):
-        ws = self.workspace(pc, gc, sc, g_on_host, out_on_host)
+        key = (pc, gc, sc, g_on_host, out_on_host)
+        ws = self.workspace(*key)
+        host = [params, exp_avg, exp_avg_sq] + ([grads] if g_on_host else []) + \
+            ([bf16_out] if out_on_host else [])
+        self._attach_host_staging(key, self.stage_pageable and not all(t.is_pinned() for t in host))
         base = ws.data_ptr()
         aligned = (base + 255) // 256 * 256
         stats = _lib.LaPipelineStats()

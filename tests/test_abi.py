@@ -30,7 +30,8 @@ def test_library_exports_every_declared_symbol():
     L = _lib.load()
     for name in declared_functions():
         assert hasattr(L, name), name
-    assert L.la_abi_version() == 1
+    version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert L.la_abi_version() == version == 2
 
 
 def test_library_is_gfx950_code_object():

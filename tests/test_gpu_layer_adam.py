@@ -374,6 +374,161 @@ def test_pinned_host_state_layer_step(hip_device):
     assert np.array_equal(adam.exp_avg_sq_flat[0].numpy().view(np.uint32), v_h.view(np.uint32))
 
 
+@pytest.mark.parametrize("pinned_p, g_host, out_host", [
+    (False, False, False),   # the reference's layout for moments: every state array pageable
+    (True, True, True),      # pinned master, pageable moments, pageable host grads and copy
+])
+def test_pageable_state_staged_through_page_locked_twins(pinned_p, g_host, out_host, hip_device):
+    """Pageable host arrays are copied by the native host threads through the
+    page-locked twins of the slots (la_pipeline_set_host_staging): same bits as
+    the runtime's own bounce path and as the oracle, over 7 chunks in 3 slots;
+    the staged byte count covers exactly the pageable arrays."""
+    from slideformer_amd.layer_adam import HostStreamer
+    n, chunk, slots = 7 * 4096 - 5, 4096, 3
+    rng = np.random.default_rng(90 + pinned_p)
+    p0 = rng.normal(0, 0.02, n).astype(np.float32)
+    m0 = rng.normal(0, 1e-3, n).astype(np.float32)
+    v0 = np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)
+    g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+    results = []
+    for stage in (True, False):
+        print(f"staged={stage} pinned_p={pinned_p} g_host={g_host} out_host={out_host}", flush=True)
+        p = torch.from_numpy(p0.copy())
+        if pinned_p:
+            p = p.pin_memory()
+        m, v = torch.from_numpy(m0.copy()), torch.from_numpy(v0.copy())
+        assert not m.is_pinned() and not v.is_pinned()
+        gd = g.clone() if g_host else g.to(hip_device)
+        out = torch.empty(n, dtype=torch.bfloat16, device="cpu" if out_host else hip_device)
+        adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+        adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=chunk, slots=slots, host_threads=3,
+                                                   stage_pageable=stage)
+        for step in (1, 2):
+            adam.step_chunk(p, gd, m, v, dict(adam.defaults, step=step), bf16_out=out)
+            st = adam.last_stream_stats
+            assert st.chunks == 7
+            if stage:
+                per_elem = (0 if pinned_p else 8) + 16 + (2 if g_host else 0) + (2 if out_host else 0)
+                assert st.staged_bytes == n * per_elem
+            else:
+                assert st.staged_bytes == 0
+        results.append([H.to_np_bits(t, k) for t, k in ((p, "f32"), (m, "f32"), (v, "f32"), (out, "bf16"))])
+    for a, b in zip(*results):
+        assert np.array_equal(a, b)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    ph, mh, vh = p0.copy(), m0.copy(), v0.copy()
+    for step in (1, 2):
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16")
+    assert np.array_equal(results[0][0], ph.view(np.uint32))
+    assert np.array_equal(results[0][1], mh.view(np.uint32))
+    assert np.array_equal(results[0][2], vh.view(np.uint32))
+    assert np.array_equal(results[0][3], O.f32_to_bf16(ph))
+
+
+def test_host_staging_rejects_bad_buffers(hip_device):
+    """la_pipeline_set_host_staging accepts only 256-byte aligned page-locked
+    memory; a staging buffer smaller than a call needs fails the call before any
+    transfer, and the host state is left untouched."""
+    import ctypes
+
+    from slideformer_amd import _lib
+    from slideformer_amd.layer_adam import HostStreamer
+
+    L = _lib.load()
+    s = HostStreamer(hip_device, chunk_elems=1024, slots=2)
+    pageable = torch.empty(1 << 20, dtype=torch.uint8)
+    pinned = torch.empty(1 << 20, dtype=torch.uint8, pin_memory=True)
+    base = (pinned.data_ptr() + 255) // 256 * 256
+    assert L.la_pipeline_set_host_staging(s.handle, pageable.data_ptr(), 1 << 19, 2) == _lib.LA_EINVAL
+    assert L.la_pipeline_set_host_staging(s.handle, base + 16, 4096, 2) == _lib.LA_EINVAL
+    assert L.la_pipeline_set_host_staging(s.handle, base, 4096, -1) == _lib.LA_EINVAL
+    assert L.la_pipeline_set_host_staging(s.handle, base, 4096, 2) == _lib.LA_OK   # too small for a call
+    n = 4096
+    p, m, v = torch.randn(n), torch.zeros(n), torch.zeros(n)
+    p_before = p.clone()
+    g = torch.zeros(n, dtype=torch.bfloat16, device=hip_device)
+    L.la_create(78, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0)
+    sc = _lib.LaScalars()
+    assert L.la_scalars(78, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.byref(sc)) == 0
+    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, False, False)
+    wbase = (ws.data_ptr() + 255) // 256 * 256
+    st = torch.cuda.current_stream(hip_device).cuda_stream
+    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
+                            _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, wbase,
+                            ws.numel() - (wbase - ws.data_ptr()), st, 1, None)
+    assert rc == _lib.LA_EINVAL
+    assert torch.equal(p, p_before) and not m.any() and not v.any()
+    assert L.la_pipeline_set_host_staging(s.handle, None, 0, 0) == _lib.LA_OK
+    L.la_destroy(78)
+
+
+def c5_layer_sizes():
+    """100B-class dense layer: hidden 12288, FFN 49152, biases, 2 LayerNorms (w, b)."""
+    h, ffn = 12288, 49152
+    return [h * 3 * h, 3 * h, h * h, h, h * ffn, ffn, ffn * h, h, h, h, h, h]
+
+
+def test_c5_streamed_full_size_matches_resident(hip_device):
+    """Config C5 at full size (1,812,099,072 params, 7.25 GB per fp32 array):
+    pinned host state streamed through HBM in 256 MB chunks x 2 slots gives the
+    same bits as the same step on HBM-resident copies, with one clip coefficient
+    from the grad norm.  Host byte offsets pass 2^32;
+    windows at the start, across element 2^30 (byte 2^32) and at the end (in
+    the short last chunk) are also checked against the oracle."""
+    from slideformer_amd.layer_adam import HostStreamer
+
+    n = sum(c5_layer_sizes())
+    assert n == 1_812_099_072 and n % 16 == 0
+    print(f"C5 streamed vs resident, n={n}", flush=True)
+    gen = torch.Generator(device=hip_device)
+    gen.manual_seed(50)
+    p_d = torch.randn(n, generator=gen, device=hip_device) * 0.02
+    m_d = torch.randn(n, generator=gen, device=hip_device) * 1e-4
+    v_d = torch.rand(n, generator=gen, device=hip_device) * 1e-8
+    g = (torch.randn(n, generator=gen, device=hip_device) * 5e-4).bfloat16()
+    windows = [(0, 4096), ((1 << 30) - 2048, (1 << 30) + 2048), (n - 4096, n)]
+    init = [[t[lo:hi].cpu().numpy().copy() for t in (p_d, m_d, v_d)] for lo, hi in windows]
+    host = []
+    for t in (p_d, m_d, v_d):
+        h = torch.empty(n, dtype=torch.float32, pin_memory=True)
+        h.copy_(t)
+        host.append(h)
+    p_h, m_h, v_h = host
+    torch.cuda.synchronize()
+    print("pinned host state ready", flush=True)
+
+    resident = LayerAdam(lr=6e-6, weight_decay=0.01)
+    coef, _ = resident.clip_grad_norm([g], 1.0)
+    out_d = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    resident.step_chunk(p_d, g, m_d, v_d, dict(resident.defaults, step=1), bf16_out=out_d, clip_coef=coef)
+    streamed = LayerAdam(lr=6e-6, weight_decay=0.01)
+    streamed._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=64 * 1024 * 1024, slots=2)
+    out_s = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    streamed.step_chunk(p_h, g, m_h, v_h, dict(streamed.defaults, step=1), bf16_out=out_s, clip_coef=coef)
+    st = streamed.last_stream_stats
+    assert st.chunks == -(-n // (64 * 1024 * 1024)) == 28 and st.h2d_bytes == st.d2h_bytes == 12 * n
+    print(f"streamed step {st.wall_ms:.1f} ms; comparing", flush=True)
+    c = float(coef.item())
+    assert 0.0 < c < 1.0
+    piece = 256 * 1024 * 1024
+    for hst, dev in ((p_h, p_d), (m_h, m_d), (v_h, v_d)):
+        for lo in range(0, n, piece):
+            hi = min(n, lo + piece)
+            assert torch.equal(hst[lo:hi].to(hip_device).view(torch.int32), dev[lo:hi].view(torch.int32)), lo
+    assert torch.equal(out_s.view(torch.int16), out_d.view(torch.int16))
+    for (lo, hi), (p0, m0, v0) in zip(windows, init):
+        orc = O.OracleAdam(6e-6, (0.9, 0.999), 1e-8, 0.01, True)
+        orc.update(1, 6e-6, 0.9, 0.999, 1e-8, 0.01, True, p0, H.to_np_bits(g[lo:hi], "bf16"), m0, v0,
+                   g16="bf16", clip_coef=c)
+        assert np.array_equal(p_h[lo:hi].numpy().view(np.uint32), p0.view(np.uint32)), lo
+        assert np.array_equal(m_h[lo:hi].numpy().view(np.uint32), m0.view(np.uint32)), lo
+        assert np.array_equal(v_h[lo:hi].numpy().view(np.uint32), v0.view(np.uint32)), lo
+        assert np.array_equal(H.to_np_bits(out_s[lo:hi], "bf16"), O.f32_to_bf16(p0)), lo
+    del p_h, m_h, v_h, host, p_d, m_d, v_d, g, out_d, out_s
+    torch._C._host_emptyCache()
+    torch.cuda.empty_cache()
+
+
 def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     """la_pipeline_step validates the dtype triple and device-pointer alignment
     up front: the host state is left untouched."""
