@@ -11,7 +11,8 @@
 // grid is one-shot (one group of 4 per lane) up to 2^22 workgroups: on gfx950
 // the vector memory counter covers loads and stores alike, so a grid-stride
 // loop would make each trip wait for the previous trip's store acknowledgements.
-// Loads and stores carry the nontemporal hint: every byte is touched once.
+// Loads and stores carry the nontemporal hint (every byte is touched once), and
+// the stores are device-scope, so they are written through the L2.
 //
 // Arithmetic follows the reference CPU Adam op for op (cpu_adam.h:159-192),
 // with explicit fmaf() and this file compiled with -ffp-contract=off; fp32
@@ -218,8 +219,19 @@ template <> struct Io<f16_t> : Io16<ConvF16> {};
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRsrcFlags = 0x00020000;          // word 3 of a gfx9 raw buffer descriptor
-constexpr int kAux = (LA_NT_LOAD ? 2 : 0);      // cache-policy bits: nt
-constexpr int kAuxSt = (LA_NT_STORE ? 2 : 0);
+// Cache-policy bits of the update kernel's buffer loads / stores (bit 0 sc0,
+// bit 1 nt, bit 4 sc1).  Loads: nt.  Stores: nt + sc1 (device scope), so the
+// results are written through instead of waiting in the L2 as dirty lines.
+// Measured on MI355X, C2 layer, same box: stores nt 0.971 ms, nt+sc1 0.960 ms,
+// nt+sc0+sc1 0.959 ms, sc1 alone 0.987 ms; the load bits made no difference.
+#ifndef LA_AUX_LOAD
+#define LA_AUX_LOAD (LA_NT_LOAD ? 2 : 0)
+#endif
+#ifndef LA_AUX_STORE
+#define LA_AUX_STORE (LA_NT_STORE ? 18 : 0)
+#endif
+constexpr int kAux = LA_AUX_LOAD;
+constexpr int kAuxSt = LA_AUX_STORE;
 
 template <typename T> struct WaveIo;
 
