@@ -77,6 +77,16 @@
 #ifndef LA_SETPRIO
 #define LA_SETPRIO 1
 #endif
+// Dynamic LDS reserved per update workgroup, unused by the kernel: it caps the
+// workgroups (= waves) resident per CU at 160 KiB / LA_UPDATE_LDS_BYTES, 16 for
+// 10 KiB.  Fewer streams in flight at once keep the HBM row buffers busier.
+// Measured on MI355X, C2 layer, same box: uncapped (32 waves per CU, the
+// register limit) 0.947 ms; 26 per CU 0.942; 20 0.918; 17-16 0.9135; 15-14
+// 0.917; 13-12 0.950-0.986; 8 1.18 ms.  Wave priority and the write-through
+// stores still add 1-3 % on top of the cap.
+#ifndef LA_UPDATE_LDS_BYTES
+#define LA_UPDATE_LDS_BYTES 10240
+#endif
 static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
 
 namespace {
@@ -590,8 +600,8 @@ int launch_step(const StepArgs& a, hipStream_t stream)
     // lanes needed: every wave takes one run of 64 groups
     const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
     const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
-    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK), 0, stream,
-                       a);
+    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
+                       LA_UPDATE_LDS_BYTES, stream, a);
     return hip_rc(hipGetLastError());
 }
 
