@@ -61,6 +61,16 @@ def cpu_baseline(n: int, budget_s: float):
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     ref = O.load_ref()
     kind = "reference" if ref is not None else "port"
     p = torch.randn(n) * 0.02
@@ -105,6 +115,10 @@ def cpu_baseline(n: int, budget_s: float):
         "sample": (f"{len(times)} whole-layer steps of {n} params (AdamW, fp32 p/m/v, bf16 grads) "
                    f"+ torch fp32->bf16 copy_, {threads} OpenMP threads on "
                    f"{os.cpu_count()} visible CPUs"),
+        "cpu_model": cpu_model,
+        "nproc": os.cpu_count(),
+        "usable_cpus": usable,
+        "omp_num_threads": threads,
         "adam_only_gparams_s": round(n / adam_s / 1e9, 4),
         "adam_ms": round(adam_s * 1e3, 3),
         "cast_ms": round(cast_s * 1e3, 3),
