@@ -33,7 +33,9 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <tuple>
 #include <unordered_map>
+#include <utility>
 
 #include "../../include/layer_adam.h"
 
@@ -593,6 +595,24 @@ uint64_t norm_workspace_bytes(uint64_t n) { return static_cast<uint64_t>(norm_gr
 
 int hip_rc(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
 
+// Launch `kernel` and return the status of this launch itself.  Arguments are
+// converted to the kernel's own parameter types and handed over by address;
+// unlike a check of hipGetLastError() after the launch, an error left behind
+// by an unrelated earlier call cannot be mistaken for a failure here.
+template <typename... KArgs, typename... Args>
+int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes, hipStream_t stream,
+           Args&&... args)
+{
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "argument count must match the kernel");
+    std::tuple<std::decay_t<KArgs>...> held(std::forward<Args>(args)...);
+    void* argv[sizeof...(KArgs)];
+    std::apply([&argv](auto&... x) {
+        int i = 0;
+        ((argv[i++] = static_cast<void*>(&x)), ...);
+    }, held);
+    return hip_rc(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds_bytes, stream));
+}
+
 template <typename TP, typename TG, typename TS>
 int launch_step(const StepArgs& a, hipStream_t stream)
 {
@@ -600,9 +620,8 @@ int launch_step(const StepArgs& a, hipStream_t stream)
     // lanes needed: every wave takes one run of 64 groups
     const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
     const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
-    hipLaunchKernelGGL((la_adamw_kernel<TP, TG, TS>), dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
-                       LA_UPDATE_LDS_BYTES, stream, a);
-    return hip_rc(hipGetLastError());
+    return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
+                  LA_UPDATE_LDS_BYTES, stream, a);
 }
 
 // The nine (param, grad, state) triples the reference registers,
@@ -711,15 +730,14 @@ int launch_norm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_
     a.max_norm = max_norm;
     a.coef = coef;
     a.norm_out = norm_out;
+    int rc;
     switch (g_dtype) {
-    case LA_F32: hipLaunchKernelGGL(la_sqnorm_kernel<float>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
-    case LA_BF16: hipLaunchKernelGGL(la_sqnorm_kernel<bf16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
-    default: hipLaunchKernelGGL(la_sqnorm_kernel<f16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    case LA_F32: rc = launch(la_sqnorm_kernel<float>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    case LA_BF16: rc = launch(la_sqnorm_kernel<bf16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    default: rc = launch(la_sqnorm_kernel<f16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
     }
-    const int rc = hip_rc(hipGetLastError());
     if (rc != LA_OK) return rc;
-    hipLaunchKernelGGL(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);
-    return hip_rc(hipGetLastError());
+    return launch(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);
 }
 
 }  // namespace
@@ -862,9 +880,10 @@ int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace, u
 int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out, la_stream_t stream)
 {
     if (!sqnorm || !coef) return LA_EINVAL;
-    hipLaunchKernelGGL(la_clip_coef_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), sqnorm,
-                       max_norm, coef, norm_out);
-    return hip_rc(hipGetLastError());
+    if ((reinterpret_cast<uintptr_t>(sqnorm) & 7u) || (reinterpret_cast<uintptr_t>(coef) & 3u)) return LA_EINVAL;
+    if (norm_out && (reinterpret_cast<uintptr_t>(norm_out) & 3u)) return LA_EINVAL;
+    return launch(la_clip_coef_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), sqnorm, max_norm,
+                  coef, norm_out);
 }
 
 }  // extern "C"

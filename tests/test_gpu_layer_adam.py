@@ -462,6 +462,43 @@ def test_host_staging_rejects_bad_buffers(hip_device):
     L.la_destroy(78)
 
 
+def test_launch_status_ignores_an_earlier_unrelated_error(hip_device):
+    """A HIP error left in the thread by an unrelated host call (here a failed
+    hipSetDevice) is not reported as a failure of the next launch.  Only
+    C-ABI calls run between planting the error and clearing it again."""
+    import ctypes
+
+    from slideformer_amd import _lib
+
+    L = _lib.load()
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = 4099
+    p = torch.randn(n, device=hip_device)
+    m = torch.zeros(n, device=hip_device)
+    v = torch.zeros(n, device=hip_device)
+    g = torch.randn(n, device=hip_device).bfloat16()
+    ws = torch.zeros(L.la_grad_sqnorm_workspace(n) // 8 + 1, dtype=torch.float64, device=hip_device)
+    sq = torch.zeros(1, dtype=torch.float64, device=hip_device)
+    coef = torch.zeros(1, device=hip_device)
+    st = torch.cuda.current_stream(hip_device).cuda_stream
+    assert L.la_create(79, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0) == 0
+    torch.cuda.synchronize()
+    try:
+        assert hip.hipSetDevice(ctypes.c_int(4096)) != 0          # invalid ordinal: fails on the host
+        assert hip.hipPeekAtLastError() != 0
+        rc_step = L.la_adam_update(79, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, _lib.LA_F32, p.data_ptr(), _lib.LA_BF16,
+                                   g.data_ptr(), _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, None, st)
+        rc_norm = L.la_grad_norm_clip(_lib.LA_BF16, g.data_ptr(), n, ws.data_ptr(), ws.numel() * 8, sq.data_ptr(),
+                                      0, 1.0, coef.data_ptr(), None, st)
+        rc_coef = L.la_clip_coef(sq.data_ptr(), 1.0, coef.data_ptr(), None, st)
+    finally:
+        hip.hipGetLastError()                                      # leave the thread clean for torch
+        L.la_destroy(79)
+    assert (rc_step, rc_norm, rc_coef) == (0, 0, 0)
+    torch.cuda.synchronize()
+    assert torch.isfinite(p).all() and sq.item() > 0 and 0.0 < coef.item() <= 1.0
+
+
 def c5_layer_sizes():
     """100B-class dense layer: hidden 12288, FFN 49152, biases, 2 LayerNorms (w, b)."""
     h, ffn = 12288, 49152
