@@ -170,20 +170,20 @@ def _unsupported(p, g, s) -> RuntimeError:
         f"and state type {_DTYPE_NAME.get(s, s)} is not supported on current hardware")
 
 
-class _ClipWorkspace:
-    """Per-device scratch for the grad-norm reduction (owned here, not by the library):
-    the per-workgroup partials and the float64 sum of squares."""
+def _torch_stream(stream, device):
+    """The stream a call runs on, as a torch stream object (None = current stream;
+    a raw hipStream_t handle is wrapped), so that scratch tensors can be
+    allocated on it and the caching allocator orders their reuse after it."""
+    if stream is None:
+        return torch.cuda.current_stream(device)
+    if isinstance(stream, torch.cuda.Stream):
+        return stream
+    return torch.cuda.ExternalStream(int(stream), device=device)
 
-    def __init__(self, device):
-        self.device = device
-        self.buf = torch.zeros(0, dtype=torch.float64, device=device)
-        self.sqnorm = torch.zeros(1, dtype=torch.float64, device=device)
 
-    def ensure(self, nbytes: int) -> torch.Tensor:
-        need = max(1, (nbytes + 7) // 8)
-        if self.buf.numel() < need:
-            self.buf = torch.zeros(need, dtype=torch.float64, device=self.device)
-        return self.buf
+def _norm_workspace_elems(lib) -> int:
+    """float64 partials for any buffer size: stage 1 never uses more workgroups than this."""
+    return max(1, lib.la_grad_sqnorm_workspace(1 << 62) // 8)
 
 
 class LayerAdam:
@@ -213,7 +213,8 @@ class LayerAdam:
         """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
         ``device``: the HIP device that updates host-resident state (default: current);
         ``pin_host_state``: allocate host-resident moments in page-locked memory
-        (faster streaming; the reference allocates pageable memory)."""
+        (streamed without staging copies; the reference allocates pageable memory,
+        which the pipeline stages through page-locked buffers)."""
         self.defaults = dict(
             lr=lr,
             bias_correction=bias_correction,
@@ -247,7 +248,6 @@ class LayerAdam:
 
         self.exp_avg_flat = OrderedDict()
         self.exp_avg_sq_flat = OrderedDict()
-        self._clip_ws: Dict[Any, _ClipWorkspace] = {}
         self._streamers: Dict[Any, HostStreamer] = {}
         # la_pipeline_stats_t of the last host-state update (timings, bytes moved)
         self.last_stream_stats = None
@@ -303,9 +303,9 @@ class LayerAdam:
         self.param_groups.append(param_group)
         layer_numel = sum(p.numel() for p in params)
         state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
-        # host moments are page-locked on request: the streaming pipeline then
-        # moves them at the host link's DMA rate instead of through bounce buffers
-        # (not with the file offload, which releases and re-allocates these buffers)
+        # host moments are page-locked on request: the copy engines then read and
+        # write them directly, without the staging copies that pageable arrays
+        # take (not with the file offload, which releases and re-allocates them)
         pin = (device.type == 'cpu' and self.pin_host_state and self.offloader is None
                and torch.cuda.is_available())
         self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device, pin_memory=pin)
@@ -594,9 +594,6 @@ class LayerAdam:
         device = grads[0].device
         if device.type != 'cuda':
             raise RuntimeError("clip_grad_norm works on device tensors")
-        ws = self._clip_ws.get(device)
-        if ws is None:
-            ws = self._clip_ws[device] = _ClipWorkspace(device)
         for g in grads:
             if g.device != device:
                 raise RuntimeError("all grads must be on one device")
@@ -605,19 +602,25 @@ class LayerAdam:
             if g.dtype not in _DTYPE_CODE:
                 raise RuntimeError(f"unsupported grad dtype {g.dtype}")
         with torch.cuda.device(device):
-            handle = _stream_handle(stream, device)
-            coef = torch.empty(1, dtype=torch.float32, device=device)
-            norm = torch.empty(1, dtype=torch.float32, device=device)
-            work = ws.ensure(max(self.lib.la_grad_sqnorm_workspace(g.numel()) for g in grads))
+            s = _torch_stream(stream, device)
+            handle = s.cuda_stream
+            # scratch of this call only, allocated on the stream it is used on:
+            # calls on different streams share nothing
+            with torch.cuda.stream(s):
+                coef = torch.empty(1, dtype=torch.float32, device=device)
+                norm = torch.empty(1, dtype=torch.float32, device=device)
+                sqnorm = torch.empty(1, dtype=torch.float64, device=device)
+                work = torch.empty(_norm_workspace_elems(self.lib), dtype=torch.float64, device=device)
             last = len(grads) - 1
             for i, g in enumerate(grads):
+                # the first buffer overwrites sqnorm, later ones add to it
                 if i < last:
                     rc = self.lib.la_grad_sqnorm(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
-                                                 work.numel() * 8, _ptr(ws.sqnorm), int(i > 0), handle)
+                                                 work.numel() * 8, _ptr(sqnorm), int(i > 0), handle)
                 else:
                     # the last buffer also writes the coefficient, in the same launch
                     rc = self.lib.la_grad_norm_clip(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
-                                                    work.numel() * 8, _ptr(ws.sqnorm), int(i > 0),
+                                                    work.numel() * 8, _ptr(sqnorm), int(i > 0),
                                                     float(max_norm), _ptr(coef), _ptr(norm), handle)
                 _lib.check(rc, "la_grad_sqnorm")
         return coef, norm
@@ -637,13 +640,18 @@ class LayerAdam:
 
 class GradNormAccumulator:
     """Float64 sum of squares accumulated over several device buffers
-    (la_grad_sqnorm with accumulate), then one clip coefficient (la_clip_coef)."""
+    (la_grad_sqnorm with accumulate), then one clip coefficient (la_clip_coef).
+
+    One accumulator is one running sum: its ``add`` and ``finish`` calls must be
+    ordered, i.e. on one stream or synchronised between streams.  Its scratch
+    is allocated once, at the size any buffer needs, so it is never freed while
+    a launch may still use it."""
 
     def __init__(self, device):
         self.lib = _lib.load()
         self.device = torch.device(device)
         self.sqnorm = torch.zeros(1, dtype=torch.float64, device=self.device)
-        self.work = torch.empty(0, dtype=torch.float64, device=self.device)
+        self.work = torch.empty(_norm_workspace_elems(self.lib), dtype=torch.float64, device=self.device)
         self.count = 0
 
     @torch.no_grad()
@@ -654,9 +662,6 @@ class GradNormAccumulator:
             raise RuntimeError("grads must be contiguous")
         if grad.dtype not in _DTYPE_CODE:
             raise RuntimeError(f"unsupported grad dtype {grad.dtype}")
-        need = max(1, self.lib.la_grad_sqnorm_workspace(grad.numel()) // 8)
-        if self.work.numel() < need:
-            self.work = torch.empty(need, dtype=torch.float64, device=self.device)
         with torch.cuda.device(self.device):
             _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[grad.dtype], _ptr(grad), grad.numel(),
                                                _ptr(self.work), self.work.numel() * 8, _ptr(self.sqnorm),

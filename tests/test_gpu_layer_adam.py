@@ -462,6 +462,29 @@ def test_host_staging_rejects_bad_buffers(hip_device):
     L.la_destroy(78)
 
 
+def test_clip_grad_norm_on_two_streams_at_once(hip_device):
+    """Two clip_grad_norm calls in flight on two streams share no scratch: each
+    coefficient equals the oracle's for its own grads."""
+    rng = np.random.default_rng(31)
+    sets = [[torch.from_numpy(rng.normal(0, s, k).astype(np.float32)).bfloat16().to(hip_device)
+             for k in (1_000_003, 77, 2_500_000)] for s in (1e-3, 5e-2)]
+    adam = LayerAdam()
+    a, b = torch.cuda.Stream(device=hip_device), torch.cuda.Stream(device=hip_device)
+    for s_ in (a, b):
+        s_.wait_stream(torch.cuda.current_stream(hip_device))
+    results = []
+    for rep in range(3):
+        ca, na = adam.clip_grad_norm(sets[0], 1.0, stream=a)
+        cb, nb = adam.clip_grad_norm(sets[1], 1.0, stream=b.cuda_stream)   # raw handle
+        results.append((ca, na, cb, nb))
+    torch.cuda.synchronize()
+    for grads, (ci, ni) in zip(sets, ((0, 1), (2, 3))):
+        sq = sum(O.grad_sqnorm(H.to_np_bits(g, "bf16"), "bf16") for g in grads)
+        c_ref, n_ref = O.clip_coef(sq, 1.0)
+        for r in results:
+            assert r[ci].item() == np.float32(c_ref) and r[ni].item() == np.float32(n_ref)
+
+
 def test_launch_status_ignores_an_earlier_unrelated_error(hip_device):
     """A HIP error left in the thread by an unrelated host call (here a failed
     hipSetDevice) is not reported as a failure of the next launch.  Only
