@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 2
+#define LA_ABI_VERSION 3
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -100,6 +100,32 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
                    float weight_decay, int bias_correction, int p_dtype, void* p, int g_dtype,
                    const void* g, int s_dtype, void* m, void* v, uint64_t n,
                    uint16_t* p_bf16_out, const float* clip_coef, la_stream_t stream);
+
+/*
+ * Several reference adam_update calls of one step in one go: segment k is the
+ * call on (p, g, m, v, n) of tensor k, in order, with the same hyper-parameters
+ * and element types, as LayerAdam.step(layer) and step_with_grad_views make
+ * them (layer_adam.py:299-327, 391-422).  Exactly equivalent to count
+ * la_adam_update calls: the beta-power state advances once per segment (also
+ * for n = 0), and each segment keeps its own scalar tail.  All segments are
+ * launched together (one launch per 16 segments), so the segments must not
+ * overlap in memory.  Every pointer is checked before anything changes; an
+ * unregistered dtype triple advances the state once and returns LA_EDTYPE,
+ * as the first of the separate calls would.
+ */
+typedef struct {
+    void* p;               /* params, p_dtype */
+    const void* g;         /* grads, g_dtype */
+    void* m;               /* exp_avg, s_dtype */
+    void* v;               /* exp_avg_sq, s_dtype */
+    uint16_t* p_bf16_out;  /* bf16 copy of the new params, nullable */
+    uint64_t n;
+} la_segment_t;
+
+int la_adam_update_multi(int id, uint64_t step, float lr, float beta1, float beta2, float eps,
+                         float weight_decay, int bias_correction, int p_dtype, int g_dtype,
+                         int s_dtype, const la_segment_t* segs, int count, const float* clip_coef,
+                         la_stream_t stream);
 
 /*
  * Grad norm (no counterpart in the reference, which has no clipping;

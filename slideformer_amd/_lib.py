@@ -32,6 +32,7 @@ EXPORTED = (
     "la_scalars",
     "la_adamw_step",
     "la_adam_update",
+    "la_adam_update_multi",
     "la_grad_sqnorm_workspace",
     "la_grad_sqnorm",
     "la_grad_norm_clip",
@@ -63,6 +64,19 @@ class LaPipelineStats(ctypes.Structure):
         ("chunks", ctypes.c_uint32),
         ("host_copy_ms", ctypes.c_float),
         ("staged_bytes", ctypes.c_uint64),
+    ]
+
+
+class LaSegment(ctypes.Structure):
+    """Mirror of ``la_segment_t``."""
+
+    _fields_ = [
+        ("p", ctypes.c_void_p),
+        ("g", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("p_bf16_out", ctypes.c_void_p),
+        ("n", ctypes.c_uint64),
     ]
 
 
@@ -109,6 +123,8 @@ def _declare(L):
     L.la_adamw_step.restype = i
     L.la_adam_update.argtypes = [i, u64, f, f, f, f, f, i, i, P, i, P, i, P, P, u64, P, P, P]
     L.la_adam_update.restype = i
+    L.la_adam_update_multi.argtypes = [i, u64, f, f, f, f, f, i, i, i, i, ctypes.POINTER(LaSegment), i, P, P]
+    L.la_adam_update_multi.restype = i
     L.la_grad_sqnorm_workspace.argtypes = [u64]
     L.la_grad_sqnorm_workspace.restype = u64
     L.la_grad_sqnorm.argtypes = [i, P, u64, P, u64, P, i, P]

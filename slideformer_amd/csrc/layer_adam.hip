@@ -36,6 +36,7 @@
 #include <tuple>
 #include <unordered_map>
 #include <utility>
+#include <vector>
 
 #include "../../include/layer_adam.h"
 
@@ -346,6 +347,62 @@ struct StepArgs {
     Coeffs k;
 };
 
+// One wave's run of 64 aligned groups (256 elements) of every stream, run w of
+// the call: loads, update, stores.  Each stream is addressed through a raw
+// buffer descriptor whose base is the run's first element (scalar registers)
+// and whose size covers only the run's valid groups, so the lanes of a partial
+// last run need no branch: their loads return 0 and their stores are dropped
+// by the hardware range check.
+template <typename TP, typename TG, typename TS>
+__device__ __forceinline__ void update_run(const StepArgs& a, uint64_t w, uint32_t lane, bool has_coef, float coef)
+{
+    const uint64_t left = a.nvec - w * 64;
+    const uint32_t nel = (left < 64 ? static_cast<uint32_t>(left) : 64u) * kVec;
+    const uint64_t e0 = a.head + w * 64 * kVec;
+    const rsrc_t rg = WaveIo<TG>::rsrc(a.g, e0, nel);
+    const rsrc_t rp = WaveIo<TP>::rsrc(a.p, e0, nel);
+    const rsrc_t rm = WaveIo<TS>::rsrc(a.m, e0, nel);
+    const rsrc_t rv = WaveIo<TS>::rsrc(a.v, e0, nel);
+    float p[kVec], g[kVec], m[kVec], v[kVec];
+#if LA_SETPRIO
+    __builtin_amdgcn_s_setprio(3);
+#endif
+    WaveIo<TG>::load4(rg, lane, g);
+    WaveIo<TP>::load4(rp, lane, p);
+    WaveIo<TS>::load4(rm, lane, m);
+    WaveIo<TS>::load4(rv, lane, v);
+#if LA_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+        const float gj = has_coef ? g[j] * coef : g[j];
+        adam_body(p[j], gj, m[j], v[j], a.k);
+    }
+    WaveIo<TP>::store4(rp, lane, p);
+    WaveIo<TS>::store4(rm, lane, m);
+    WaveIo<TS>::store4(rv, lane, v);
+    if (a.out) WaveIo<bf16_t>::store4(WaveIo<bf16_t>::rsrc(a.out, e0, nel), lane, p);
+}
+
+// One element outside the aligned groups; the reference's scalar tail from
+// a.tail_start on, its SIMD body order before.
+template <typename TP, typename TG, typename TS>
+__device__ __forceinline__ void update_one(const StepArgs& a, uint64_t e, bool has_coef, float coef)
+{
+    float g = Io<TG>::load1(a.g, e);
+    if (has_coef) g = g * coef;
+    float p = Io<TP>::load1(a.p, e);
+    float m = Io<TS>::load1(a.m, e);
+    float v = Io<TS>::load1(a.v, e);
+    if (e >= a.tail_start) adam_tail(p, g, m, v, a.k);
+    else adam_body(p, g, m, v, a.k);
+    Io<TP>::store1(a.p, e, p);
+    Io<TS>::store1(a.m, e, m);
+    Io<TS>::store1(a.v, e, v);
+    if (a.out) a.out[e] = static_cast<uint16_t>(f32_to_bf16_bits(p));
+}
+
 template <typename TP, typename TG, typename TS>
 __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
 {
@@ -354,60 +411,59 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
 
-    // Wave w owns groups [64w, 64w + 64): one lane-contiguous run of 256
-    // elements per stream.  Each stream is addressed through a raw buffer
-    // descriptor whose base is the wave's first element (scalar registers) and
-    // whose size covers only the wave's valid groups, so the lanes of a partial
-    // last wave need no branch: their loads return 0 and their stores are
-    // dropped by the hardware range check.
+    // Wave w owns run w: groups [64w, 64w + 64), 256 lane-contiguous elements
+    // per stream.  The grid is one-shot unless n exceeds LA_MAX_GRID runs.
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t nwaves = stride >> 6;
-    for (uint64_t w = tid >> 6; w * 64 < a.nvec; w += nwaves) {
-        const uint64_t left = a.nvec - w * 64;
-        const uint32_t nel = (left < 64 ? static_cast<uint32_t>(left) : 64u) * kVec;
-        const uint64_t e0 = a.head + w * 64 * kVec;
-        const rsrc_t rg = WaveIo<TG>::rsrc(a.g, e0, nel);
-        const rsrc_t rp = WaveIo<TP>::rsrc(a.p, e0, nel);
-        const rsrc_t rm = WaveIo<TS>::rsrc(a.m, e0, nel);
-        const rsrc_t rv = WaveIo<TS>::rsrc(a.v, e0, nel);
-        float p[kVec], g[kVec], m[kVec], v[kVec];
-#if LA_SETPRIO
-        __builtin_amdgcn_s_setprio(3);
-#endif
-        WaveIo<TG>::load4(rg, lane, g);
-        WaveIo<TP>::load4(rp, lane, p);
-        WaveIo<TS>::load4(rm, lane, m);
-        WaveIo<TS>::load4(rv, lane, v);
-#if LA_SETPRIO
-        __builtin_amdgcn_s_setprio(0);
-#endif
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-            const float gj = has_coef ? g[j] * coef : g[j];
-            adam_body(p[j], gj, m[j], v[j], a.k);
-        }
-        WaveIo<TP>::store4(rp, lane, p);
-        WaveIo<TS>::store4(rm, lane, m);
-        WaveIo<TS>::store4(rv, lane, v);
-        if (a.out) WaveIo<bf16_t>::store4(WaveIo<bf16_t>::rsrc(a.out, e0, nel), lane, p);
-    }
+    for (uint64_t w = tid >> 6; w * 64 < a.nvec; w += nwaves) update_run<TP, TG, TS>(a, w, lane, has_coef, coef);
 
     // Elements outside the aligned groups: [0, head) and [head + 4*nvec, n).
     const uint64_t vec_end = a.head + a.nvec * kVec;
     const uint64_t nscalar = a.head + (a.n - vec_end);
     for (uint64_t s = tid; s < nscalar; s += stride) {
         const uint64_t e = s < a.head ? s : vec_end + (s - a.head);
-        float g = Io<TG>::load1(a.g, e);
-        if (has_coef) g = g * coef;
-        float p = Io<TP>::load1(a.p, e);
-        float m = Io<TS>::load1(a.m, e);
-        float v = Io<TS>::load1(a.v, e);
-        if (e >= a.tail_start) adam_tail(p, g, m, v, a.k);
-        else adam_body(p, g, m, v, a.k);
-        Io<TP>::store1(a.p, e, p);
-        Io<TS>::store1(a.m, e, m);
-        Io<TS>::store1(a.v, e, v);
-        if (a.out) a.out[e] = static_cast<uint16_t>(f32_to_bf16_bits(p));
+        update_one<TP, TG, TS>(a, e, has_coef, coef);
+    }
+}
+
+// Several calls of one step in one launch: the tensors of a layer, each its
+// own reference adam_update call with its own scalars (the beta-power state
+// advances once per call) and its own scalar tail.  Waves [run_begin[s],
+// run_begin[s+1]) take the runs of segment s; then one wave per segment takes
+// its at most 21 elements outside the aligned groups.  Segments must not
+// overlap in memory.
+constexpr int kMaxSegs = 16;
+constexpr uint64_t kMaxSegScalars = 64;  // one wave's lanes
+
+struct MultiArgs {
+    const float* coef;
+    uint32_t count;
+    uint64_t run_begin[kMaxSegs + 1];
+    StepArgs seg[kMaxSegs];
+};
+
+template <typename TP, typename TG, typename TS>
+__global__ __launch_bounds__(LA_BLOCK) void la_adamw_multi_kernel(MultiArgs a)
+{
+    const bool has_coef = a.coef != nullptr;
+    const float coef = has_coef ? *a.coef : 1.0f;
+    const uint64_t w = (static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t runs = a.run_begin[a.count];
+    if (w < runs) {
+        uint32_t s = 0;
+        while (w >= a.run_begin[s + 1]) ++s;
+        update_run<TP, TG, TS>(a.seg[s], w - a.run_begin[s], lane, has_coef, coef);
+        return;
+    }
+    const uint64_t s = w - runs;
+    if (s >= a.count) return;
+    const StepArgs& sa = a.seg[s];
+    const uint64_t vec_end = sa.head + sa.nvec * kVec;
+    const uint64_t nscalar = sa.head + (sa.n - vec_end);
+    if (lane < nscalar) {
+        const uint64_t e = lane < sa.head ? lane : vec_end + (lane - sa.head);
+        update_one<TP, TG, TS>(sa, e, has_coef, coef);
     }
 }
 
@@ -613,35 +669,93 @@ int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes, 
     return hip_rc(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds_bytes, stream));
 }
 
-template <typename TP, typename TG, typename TS>
-int launch_step(const StepArgs& a, hipStream_t stream)
-{
-    const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-    // lanes needed: every wave takes one run of 64 groups
-    const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
-    const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
-    return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
-                  LA_UPDATE_LDS_BYTES, stream, a);
-}
+template <typename TP, typename TG, typename TS> struct StepLauncher {
+    static int run(const StepArgs& a, hipStream_t stream)
+    {
+        const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
+        // lanes needed: every wave takes one run of 64 groups
+        const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
+        const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
+        return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
+                      LA_UPDATE_LDS_BYTES, stream, a);
+    }
+};
+
+template <typename TP, typename TG, typename TS> struct MultiLauncher {
+    // waves: runs of every segment + one scalar wave per segment
+    static int run(const MultiArgs& a, uint64_t waves, hipStream_t stream)
+    {
+        return launch(la_adamw_multi_kernel<TP, TG, TS>, dim3(static_cast<uint32_t>(waves * 64 / LA_BLOCK)),
+                      dim3(LA_BLOCK), LA_UPDATE_LDS_BYTES, stream, a);
+    }
+};
 
 // The nine (param, grad, state) triples the reference registers,
 // cpu_adam_impl.cpp:181-189; nothing else is instantiated.
-int dispatch_step(int p, int g, int s, const StepArgs& a, hipStream_t st)
+template <template <typename, typename, typename> class L, typename... Args>
+int dispatch_triple(int p, int g, int s, Args&&... args)
 {
     if (p == LA_F32 && s == LA_F32) {
-        if (g == LA_BF16) return launch_step<float, bf16_t, float>(a, st);
-        if (g == LA_F32) return launch_step<float, float, float>(a, st);
-        if (g == LA_F16) return launch_step<float, f16_t, float>(a, st);
+        if (g == LA_BF16) return L<float, bf16_t, float>::run(args...);
+        if (g == LA_F32) return L<float, float, float>::run(args...);
+        if (g == LA_F16) return L<float, f16_t, float>::run(args...);
     } else if (p == LA_BF16) {
-        if (g == LA_BF16 && s == LA_F32) return launch_step<bf16_t, bf16_t, float>(a, st);
-        if (g == LA_F32 && s == LA_F32) return launch_step<bf16_t, float, float>(a, st);
-        if (g == LA_BF16 && s == LA_BF16) return launch_step<bf16_t, bf16_t, bf16_t>(a, st);
+        if (g == LA_BF16 && s == LA_F32) return L<bf16_t, bf16_t, float>::run(args...);
+        if (g == LA_F32 && s == LA_F32) return L<bf16_t, float, float>::run(args...);
+        if (g == LA_BF16 && s == LA_BF16) return L<bf16_t, bf16_t, bf16_t>::run(args...);
     } else if (p == LA_F16) {
-        if (g == LA_F16 && s == LA_F32) return launch_step<f16_t, f16_t, float>(a, st);
-        if (g == LA_F32 && s == LA_F32) return launch_step<f16_t, float, float>(a, st);
-        if (g == LA_F16 && s == LA_F16) return launch_step<f16_t, f16_t, f16_t>(a, st);
+        if (g == LA_F16 && s == LA_F32) return L<f16_t, f16_t, float>::run(args...);
+        if (g == LA_F32 && s == LA_F32) return L<f16_t, float, float>::run(args...);
+        if (g == LA_F16 && s == LA_F16) return L<f16_t, f16_t, f16_t>::run(args...);
     }
     return LA_EDTYPE;
+}
+
+// Check the pointers of one call and lay out its elements (everything of
+// StepArgs but the coefficients).  n > 0.
+int prepare_step(int p_dtype, void* p, int g_dtype, const void* g, int s_dtype, void* m, void* v, uint64_t n,
+                 uint16_t* p_bf16_out, const float* clip_coef, StepArgs& a)
+{
+    if (!p || !g || !m || !v) return LA_EINVAL;
+    const uintptr_t addr[5] = {reinterpret_cast<uintptr_t>(p), reinterpret_cast<uintptr_t>(g),
+                               reinterpret_cast<uintptr_t>(m), reinterpret_cast<uintptr_t>(v),
+                               reinterpret_cast<uintptr_t>(p_bf16_out)};
+    const int bytes[5] = {elem_bytes(p_dtype), elem_bytes(g_dtype), elem_bytes(s_dtype), elem_bytes(s_dtype), 2};
+    const int count = p_bf16_out ? 5 : 4;
+    for (int i = 0; i < count; ++i)
+        if (addr[i] % static_cast<uintptr_t>(bytes[i]) != 0) return LA_EINVAL;
+    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
+    a.p = p;
+    a.g = g;
+    a.m = m;
+    a.v = v;
+    a.out = p_bf16_out;
+    a.coef = clip_coef;
+    a.n = n;
+    a.tail_start = n - n % 16;
+    const int h = common_head(addr, bytes, count);
+    if (h < 0 || static_cast<uint64_t>(h) >= a.tail_start) {
+        a.head = 0;
+        a.nvec = 0;
+    } else {
+        a.head = static_cast<uint64_t>(h);
+        a.nvec = (a.tail_start - a.head) / kVec;
+    }
+    return LA_OK;
+}
+
+void set_coeffs(const la_scalars_t& sc, Coeffs& k)
+{
+    k.b1 = sc.beta1;
+    k.b2 = sc.beta2;
+    k.omb1 = sc.one_minus_beta1;
+    k.omb2 = sc.one_minus_beta2;
+    k.bc2 = sc.bias_correction2;
+    k.eps = sc.eps;
+    k.step_size = sc.step_size;
+    k.w_decay = sc.w_decay;
+    k.wd = sc.weight_decay;
+    k.mode = sc.decay_mode;
 }
 
 bool triple_registered(int p, int g, int s)
@@ -806,45 +920,12 @@ int la_adamw_step(const la_scalars_t* sc, int p_dtype, void* p, int g_dtype, con
     if (!dt_valid(p_dtype) || !dt_valid(g_dtype) || !dt_valid(s_dtype)) return LA_EDTYPE;
     if (!triple_registered(p_dtype, g_dtype, s_dtype)) return LA_EDTYPE;
     if (n == 0) return LA_OK;
-    if (!p || !g || !m || !v) return LA_EINVAL;
-
-    const uintptr_t addr[5] = {reinterpret_cast<uintptr_t>(p), reinterpret_cast<uintptr_t>(g),
-                               reinterpret_cast<uintptr_t>(m), reinterpret_cast<uintptr_t>(v),
-                               reinterpret_cast<uintptr_t>(p_bf16_out)};
-    const int bytes[5] = {elem_bytes(p_dtype), elem_bytes(g_dtype), elem_bytes(s_dtype), elem_bytes(s_dtype), 2};
-    const int count = p_bf16_out ? 5 : 4;
-    for (int i = 0; i < count; ++i)
-        if (addr[i] % static_cast<uintptr_t>(bytes[i]) != 0) return LA_EINVAL;
-    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
 
     StepArgs a;
-    a.p = p;
-    a.g = g;
-    a.m = m;
-    a.v = v;
-    a.out = p_bf16_out;
-    a.coef = clip_coef;
-    a.n = n;
-    a.tail_start = n - n % 16;
-    const int h = common_head(addr, bytes, count);
-    if (h < 0 || static_cast<uint64_t>(h) >= a.tail_start) {
-        a.head = 0;
-        a.nvec = 0;
-    } else {
-        a.head = static_cast<uint64_t>(h);
-        a.nvec = (a.tail_start - a.head) / kVec;
-    }
-    a.k.b1 = sc->beta1;
-    a.k.b2 = sc->beta2;
-    a.k.omb1 = sc->one_minus_beta1;
-    a.k.omb2 = sc->one_minus_beta2;
-    a.k.bc2 = sc->bias_correction2;
-    a.k.eps = sc->eps;
-    a.k.step_size = sc->step_size;
-    a.k.w_decay = sc->w_decay;
-    a.k.wd = sc->weight_decay;
-    a.k.mode = sc->decay_mode;
-    return dispatch_step(p_dtype, g_dtype, s_dtype, a, static_cast<hipStream_t>(stream));
+    const int rc = prepare_step(p_dtype, p, g_dtype, g, s_dtype, m, v, n, p_bf16_out, clip_coef, a);
+    if (rc != LA_OK) return rc;
+    set_coeffs(*sc, a.k);
+    return dispatch_triple<StepLauncher>(p_dtype, g_dtype, s_dtype, a, static_cast<hipStream_t>(stream));
 }
 
 int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
@@ -857,6 +938,83 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
     int rc = la_scalars(id, step, lr, beta1, beta2, eps, weight_decay, bias_correction, &sc);
     if (rc != LA_OK) return rc;
     return la_adamw_step(&sc, p_dtype, p, g_dtype, g, s_dtype, m, v, n, p_bf16_out, clip_coef, stream);
+}
+
+int la_adam_update_multi(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                         int bias_correction, int p_dtype, int g_dtype, int s_dtype, const la_segment_t* segs,
+                         int count, const float* clip_coef, la_stream_t stream)
+{
+    if (count < 0 || (count > 0 && !segs)) return LA_EINVAL;
+    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
+    const bool registered = dt_valid(p_dtype) && dt_valid(g_dtype) && dt_valid(s_dtype) &&
+                            triple_registered(p_dtype, g_dtype, s_dtype);
+    std::vector<StepArgs> args(registered ? static_cast<size_t>(count) : 0);
+    if (registered) {
+        // every pointer is checked before anything changes
+        for (int k = 0; k < count; ++k) {
+            const la_segment_t& q = segs[k];
+            if (q.n == 0) {
+                args[k].n = 0;
+                continue;
+            }
+            const int rc = prepare_step(p_dtype, q.p, g_dtype, q.g, s_dtype, q.m, q.v, q.n, q.p_bf16_out,
+                                        clip_coef, args[k]);
+            if (rc != LA_OK) return rc;
+        }
+    }
+    {
+        // the beta-power state advances once per segment, as separate calls would
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_states.find(id);
+        if (it == g_states.end()) return LA_EINVAL;
+        if (!registered) {
+            // the first call of the sequence would advance the state, then fail
+            // on the triple (cpu_adam_impl.cpp:241-261)
+            la_scalars_t sc;
+            if (count > 0) derive_scalars(it->second, step, lr, beta1, beta2, eps, weight_decay, bias_correction, &sc);
+            return LA_EDTYPE;
+        }
+        for (int k = 0; k < count; ++k) {
+            la_scalars_t sc;
+            derive_scalars(it->second, step, lr, beta1, beta2, eps, weight_decay, bias_correction, &sc);
+            set_coeffs(sc, args[k].k);
+        }
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    MultiArgs batch;
+    std::memset(&batch, 0, sizeof(batch));
+    batch.coef = clip_coef;
+    uint64_t runs = 0;
+    auto flush = [&]() -> int {
+        if (batch.count == 0) return LA_OK;
+        batch.run_begin[batch.count] = runs;
+        const int rc = dispatch_triple<MultiLauncher>(p_dtype, g_dtype, s_dtype, batch, runs + batch.count, st);
+        std::memset(&batch, 0, sizeof(batch));
+        batch.coef = clip_coef;
+        runs = 0;
+        return rc;
+    };
+    for (int k = 0; k < count; ++k) {
+        const StepArgs& a = args[k];
+        if (a.n == 0) continue;
+        const uint64_t seg_runs = (a.nvec + 63) / 64;
+        const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
+        if (nscalar > kMaxSegScalars || seg_runs > LA_MAX_GRID / 2) {
+            // pointers out of phase (all elements scalar) or a huge segment: its own launch
+            const int rc = dispatch_triple<StepLauncher>(p_dtype, g_dtype, s_dtype, a, st);
+            if (rc != LA_OK) return rc;
+            continue;
+        }
+        if (batch.count == static_cast<uint32_t>(kMaxSegs) || runs + seg_runs > LA_MAX_GRID / 2) {
+            const int rc = flush();
+            if (rc != LA_OK) return rc;
+        }
+        batch.run_begin[batch.count] = runs;
+        batch.seg[batch.count] = a;
+        batch.count++;
+        runs += seg_runs;
+    }
+    return flush();
 }
 
 uint64_t la_grad_sqnorm_workspace(uint64_t n) { return norm_workspace_bytes(n); }

@@ -170,6 +170,31 @@ def _unsupported(p, g, s) -> RuntimeError:
         f"and state type {_DTYPE_NAME.get(s, s)} is not supported on current hardware")
 
 
+def _batchable(entries) -> bool:
+    """True when the (params, grads, exp_avg, exp_avg_sq) tensors can go to
+    la_adam_update_multi: one HIP device, one registered dtype triple, contiguous,
+    matching sizes, and no two tensors written by the update overlap."""
+    p0, g0, m0, _ = entries[0]
+    if p0.device.type != 'cuda':
+        return False
+    key = (p0.dtype, g0.dtype, m0.dtype)
+    if key not in SUPPORTED_TRIPLES:
+        return False
+    spans = []
+    for p, g, m, v in entries:
+        n = p.numel()
+        for t in (p, g, m, v):
+            if t.device != p0.device or not t.is_contiguous() or t.numel() != n:
+                return False
+        if (p.dtype, g.dtype, m.dtype) != key or v.dtype != m.dtype:
+            return False
+        for t in (p, m, v):
+            if n:
+                spans.append((t.data_ptr(), t.data_ptr() + n * t.element_size()))
+    spans.sort()
+    return all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+
+
 def _torch_stream(stream, device):
     """The stream a call runs on, as a torch stream object (None = current stream;
     a raw hipStream_t handle is wrapped), so that scratch tensors can be
@@ -497,17 +522,15 @@ class LayerAdam:
             groups = self.param_groups
         self._pre_step(layer_idx)
         for param_group in groups:
-            beta1, beta2 = param_group['betas']
             param_group['step'] += 1
+            entries = []
             for p in param_group['params']:
                 if p.grad is None:
                     continue
                 state = self.state[p]
                 assert p.data.numel() == p.grad.data.numel(), "params and grads must have the same size"
-                self.adam_update(param_group['step'], param_group['lr'], beta1, beta2,
-                                 param_group['eps'], param_group['weight_decay'],
-                                 param_group['bias_correction'], p.data, p.grad.data,
-                                 state['exp_avg'], state['exp_avg_sq'])
+                entries.append((p.data, p.grad.data, state['exp_avg'], state['exp_avg_sq']))
+            self._update_tensors(param_group, entries)
         self._post_step(layer_idx)
         return loss
 
@@ -526,8 +549,8 @@ class LayerAdam:
             groups = self.param_groups
         self._pre_step(layer_idx)
         for param_group in groups:
-            beta1, beta2 = param_group['betas']
             param_group['step'] += 1
+            entries = []
             for p in param_group['params']:
                 grad = grad_views.get(p) if grad_views else None
                 if grad is None:
@@ -535,12 +558,38 @@ class LayerAdam:
                     continue
                 state = self.state[p]
                 assert p.data.numel() == grad.numel(), "params and grads must have the same size"
-                self.adam_update(param_group['step'], param_group['lr'], beta1, beta2,
-                                 param_group['eps'], param_group['weight_decay'],
-                                 param_group['bias_correction'], p.data, grad,
-                                 state['exp_avg'], state['exp_avg_sq'])
+                entries.append((p.data, grad, state['exp_avg'], state['exp_avg_sq']))
+            self._update_tensors(param_group, entries)
         self._post_step(layer_idx)
         return loss
+
+    def _update_tensors(self, param_group, entries):
+        """The per-tensor adam_update calls of step(layer) / step_with_grad_views
+        (layer_adam.py:314-327, 397-410), in order.  Device tensors on one device
+        with one registered dtype triple that pass every per-call check and do not
+        overlap go to the library as one la_adam_update_multi call: the same
+        results and the same beta-power state as separate calls, in one or two
+        launches.  Anything else takes the per-call path, which raises the
+        reference's errors where the reference raises them."""
+        beta1, beta2 = param_group['betas']
+        hp = (param_group['step'], param_group['lr'], beta1, beta2, param_group['eps'],
+              param_group['weight_decay'], param_group['bias_correction'])
+        if len(entries) > 1 and _batchable(entries):
+            p0, g0, m0, _ = entries[0]
+            segs = (_lib.LaSegment * len(entries))()
+            for k, (p, g, m, v) in enumerate(entries):
+                segs[k].p, segs[k].g, segs[k].m, segs[k].v = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
+                segs[k].p_bf16_out = None
+                segs[k].n = p.numel()
+            with torch.cuda.device(p0.device):
+                rc = self.lib.la_adam_update_multi(
+                    self.optimizer_id, int(hp[0]), hp[1], hp[2], hp[3], hp[4], hp[5], int(bool(hp[6])),
+                    _DTYPE_CODE[p0.dtype], _DTYPE_CODE[g0.dtype], _DTYPE_CODE[m0.dtype], segs, len(entries),
+                    None, _stream_handle(None, p0.device))
+            _lib.check(rc, "la_adam_update_multi")
+            return
+        for p, g, m, v in entries:
+            self.adam_update(*hp, p, g, m, v)
 
     @torch.no_grad()
     def begin_chunk_step(self, layer_idx: int):

@@ -55,12 +55,26 @@ class HipAdam:
             st.cuda_stream)
         _lib.check(rc, "la_adam_update")
 
+    def update_multi(self, step, lr, b1, b2, eps, wd, bc, tensors, *, coef=None, stream=None):
+        """One la_adam_update_multi call over [(p, g, m, v, out-or-None), ...]."""
+        kinds = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+        p0, g0, m0 = tensors[0][:3]
+        segs = (_lib.LaSegment * len(tensors))()
+        for k, (p, g, m, v, out) in enumerate(tensors):
+            segs[k].p, segs[k].g, segs[k].m, segs[k].v = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
+            segs[k].p_bf16_out = None if out is None else out.data_ptr()
+            segs[k].n = p.numel()
+        st = stream if stream is not None else torch.cuda.current_stream(p0.device)
+        rc = self.L.la_adam_update_multi(
+            self.id, int(step), lr, b1, b2, eps, wd, int(bool(bc)), CODE[kinds[p0.dtype]], CODE[kinds[g0.dtype]],
+            CODE[kinds[m0.dtype]], segs, len(tensors), None if coef is None else coef.data_ptr(), st.cuda_stream)
+        _lib.check(rc, "la_adam_update_multi")
+
 
 def sqnorm(g: torch.Tensor, accumulate_into: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Sum of squares of a device grad buffer in float64 (device scalar)."""
     L = _lib.load()
     kinds = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
-    # the workspace's ticket word must start at zero
     ws = torch.zeros(max(1, L.la_grad_sqnorm_workspace(g.numel()) // 8), dtype=torch.float64,
                      device=g.device)
     out = accumulate_into if accumulate_into is not None else torch.zeros(1, dtype=torch.float64,

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
-    assert L.la_abi_version() == version == 2
+    assert L.la_abi_version() == version == 3
 
 
 def test_library_is_gfx950_code_object():
@@ -122,3 +122,54 @@ def test_grad_sqnorm_workspace_is_bounded():
     assert all(w % 8 == 0 and w >= 8 for w in ws)
     assert ws == sorted(ws)                         # non-decreasing in n
     assert ws[-1] == L.la_grad_sqnorm_workspace(1 << 35) <= 64 * 1024   # capped
+
+
+def _segments(specs):
+    segs = (_lib.LaSegment * len(specs))()
+    for k, (p, g, m, v, out, n) in enumerate(specs):
+        segs[k].p, segs[k].g, segs[k].m, segs[k].v, segs[k].p_bf16_out, segs[k].n = p, g, m, v, out, n
+    return segs
+
+
+def test_multi_update_host_logic_without_launch():
+    """la_adam_update_multi: argument checks come before any state change, and
+    the beta-power state advances once per segment, n = 0 segments included,
+    exactly as the same number of la_adam_update calls would."""
+    L = _lib.load()
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    lib = O.lib()
+    L.la_create(904, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0)
+    replay = []
+
+    def scalars(step):
+        sc = _scalars(L, 904, step, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+        replay.append(step)
+        return sc
+
+    for st in range(1, 5):
+        scalars(st)
+    args = (904, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0, 1, 0)
+    assert L.la_adam_update_multi(*args, None, -1, None, None) == _lib.LA_EINVAL
+    assert L.la_adam_update_multi(*args, None, 2, None, None) == _lib.LA_EINVAL
+    # a misaligned pointer in the second segment: rejected, nothing advanced
+    bad = _segments([(0x1000, 0x2000, 0x3000, 0x4000, None, 8), (0x1001, 0x2000, 0x3000, 0x4000, None, 8)])
+    assert L.la_adam_update_multi(*args, bad, 2, None, None) == _lib.LA_EINVAL
+    # unknown id: nothing to advance
+    assert L.la_adam_update_multi(123457, *args[1:], _segments([(None,) * 5 + (0,)]), 1, None, None) == _lib.LA_EINVAL
+    # three empty segments: no launch, three state advances
+    assert L.la_adam_update_multi(*args, _segments([(None,) * 5 + (0,)] * 3), 3, None, None) == 0
+    replay += [5, 5, 5]
+    # an unregistered triple advances the state once, then fails like the first separate call
+    assert L.la_adam_update_multi(904, 6, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0, 0, 1,
+                                  _segments([(None,) * 5 + (0,)] * 2), 2, None, None) == _lib.LA_EDTYPE
+    replay += [6]
+    got = scalars(7)
+    for st in replay:
+        lib.orc_increment_step(orc.s, st, 0.9, 0.999)
+        lib.orc_update_state(orc.s, 1e-3, 1e-8, 0.01, 1)
+    ref = orc.scalars()
+    vals = np.array([got.beta1_t, got.beta2_t, got.bias_correction1, got.bias_correction2, got.step_size,
+                     got.w_decay, got.one_minus_beta1, got.one_minus_beta2], dtype=np.float32)
+    assert np.array_equal(vals.view(np.uint32), ref.view(np.uint32))
+    assert got.step == orc.s.step == 7
+    L.la_destroy(904)

@@ -418,3 +418,69 @@ def test_single_call_beyond_2_pow_31_elements(hip_device):
         assert np.array_equal(H.to_np_bits(v[a:b], "f32"), vh.view(np.uint32)), (a, b)
     del p, g, m, v
     torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# several calls of one step in one launch (la_adam_update_multi)
+# ---------------------------------------------------------------------------
+
+MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 2, 5000, 12, 129, 31, 8]
+
+
+@pytest.mark.parametrize("triple", [("f32", "bf16", "f32"), ("f32", "f32", "f32"), ("bf16", "bf16", "bf16")])
+def test_multi_update_equals_separate_calls(triple, hip_device):
+    """20 segments (two launches of up to 16) of awkward sizes, some at odd
+    element offsets inside their buffers and one whose params are out of phase
+    with its grads (its own launch), with a clip coefficient and bf16 copies on
+    every other segment: bit-exact with the same 20 la_adam_update calls, and
+    every segment with the oracle replaying those calls."""
+    pk, gk, sk = triple
+    td = {"f32": torch.float32, "bf16": torch.bfloat16}
+    log(f"multi-update {triple}")
+    coef = torch.tensor([0.37], device=hip_device)
+
+    def make():
+        torch.manual_seed(11)
+        segs = []
+        for k, n in enumerate(MULTI_SIZES):
+            off = (k * 3) % 4                                 # odd offsets inside a larger buffer
+            goff = (off + 1) % 4 if k == 9 else off           # segment 9: params out of phase with grads
+            def buf(dt, o, std):
+                return (torch.randn(n + 8, device=hip_device) * std).to(td[dt])[o:o + n]
+            p = buf(pk, off, 0.02)
+            g = buf(gk, goff, 1e-3)
+            m = buf(sk, off, 1e-3)
+            v = buf(sk, off, 1e-3).abs_()
+            out = torch.empty(n + 4, dtype=torch.bfloat16, device=hip_device)[off:off + n] if k % 2 else None
+            segs.append([p, g, m, v, out])
+        return segs
+
+    a, b = make(), make()
+    opt_a = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    opt_b = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        opt_a.update_multi(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, a, coef=coef)
+        for p, g, m, v, out in b:
+            opt_b.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, out=out, coef=coef)
+    torch.cuda.synchronize()
+    for k, (sa, sb) in enumerate(zip(a, b)):
+        for i, kind in enumerate((pk, sk, sk)):
+            assert np.array_equal(H.to_np_bits(sa[(0, 2, 3)[i]], kind), H.to_np_bits(sb[(0, 2, 3)[i]], kind)), (k, i)
+        if sa[4] is not None:
+            assert np.array_equal(H.to_np_bits(sa[4], "bf16"), H.to_np_bits(sb[4], "bf16")), k
+    # absolute check against the oracle, replaying the same 20 calls per step
+    c = make()
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    hp = [H.to_np_bits(s[0], pk) for s in c]
+    hm = [H.to_np_bits(s[2], sk) for s in c]
+    hv = [H.to_np_bits(s[3], sk) for s in c]
+    hg = [H.to_np_bits(s[1], gk) for s in c]
+    for step in (1, 2, 3):
+        for k in range(len(c)):
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, _view(hp[k], pk), _view(hg[k], gk),
+                       _view(hm[k], sk), _view(hv[k], sk), p16=KIND16[pk], g16=KIND16[gk], s16=KIND16[sk],
+                       clip_coef=0.37)
+    for k in range(len(c)):
+        assert np.array_equal(H.to_np_bits(a[k][0], pk), hp[k]), k
+        assert np.array_equal(H.to_np_bits(a[k][2], sk), hm[k]), k
+        assert np.array_equal(H.to_np_bits(a[k][3], sk), hv[k]), k
