@@ -463,6 +463,87 @@ def resident_stack(args):
     print(json.dumps(res), flush=True)
 
 
+GPT2_BLOCK = [(768,), (768,), (2304, 768), (2304,), (768, 768), (768,), (768,), (768,), (3072, 768), (3072,),
+              (768, 3072), (768,)]  # ln_1, c_attn, c_proj, ln_2, c_fc, c_proj (scripts/custom_gpt_model.py:80-145)
+LLAMA8B_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
+                  (4096, 14336), (4096,), (4096,)]
+
+
+def step_api(args):
+    """The per-tensor entry points on one layer of separate device tensors:
+    LayerAdam.step(layer) (fp32 p.grad, layer_adam.py:271-359) and
+    step_with_grad_views (bf16 grad views, :362-428) -- both one
+    la_adam_update_multi call per layer -- against one adam_update call per
+    tensor (the reference's loop) and against step_chunk on the same layer
+    held flat.  C1 = a GPT-2-small block (12 tensors), C2 = a Llama-3.1-8B
+    layer (9 tensors)."""
+    import torch
+
+    from slideformer_amd import LayerAdam
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    shapes = GPT2_BLOCK if args.step_api == "c1" else LLAMA8B_SHAPES
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(80)
+    params = [torch.nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
+    for p in params:
+        p.grad = torch.randn(p.shape, generator=gen, device=dev) * 1e-3
+    views = {p: (torch.randn(p.shape, generator=gen, device=dev) * 1e-3).bfloat16() for p in params}
+    n = sum(p.numel() for p in params)
+    adam = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    adam.add_layer_params(0, params)
+    flat = [torch.randn(n, generator=gen, device=dev) * 0.02, (torch.randn(n, generator=gen, device=dev) * 1e-3)
+            .bfloat16(), torch.zeros(n, device=dev), torch.zeros(n, device=dev)]
+    group = adam.param_groups[0]
+
+    def per_call():
+        # the reference's loop: one adam_update call per tensor
+        group['step'] += 1
+        for p in params:
+            st = adam.state[p]
+            adam.adam_update(group['step'], group['lr'], 0.9, 0.999, group['eps'], group['weight_decay'],
+                             group['bias_correction'], p.data, p.grad.data, st['exp_avg'], st['exp_avg_sq'])
+
+    cases = {
+        "step(layer), fp32 grads": lambda: adam.step(0),
+        "step_with_grad_views, bf16 grads": lambda: adam.step_with_grad_views(0, views),
+        "one adam_update per tensor, fp32 grads": per_call,
+        "step_chunk on the flat layer, bf16 grads": lambda: adam.step_chunk(*flat, group),
+    }
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, fn in cases.items():
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        a.record(stream)
+        for _ in range(args.steps):
+            fn()
+        b.record(stream)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        res[name] = {"us_per_step": round(a.elapsed_time(b) / args.steps * 1e3, 1),
+                     "host_issue_us_per_step": round((t1 - t0) / args.steps * 1e6, 1),
+                     "wall_us_per_step": round((t2 - t0) / args.steps * 1e6, 1)}
+        log(f"{name}: {res[name]}")
+    print(json.dumps({
+        "metric": "LayerAdam per-tensor entry points, us per layer step (HIP events)",
+        "unit": "us",
+        "higher_is_better": False,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "data": "synthetic",
+        "config": {"workload": ("C1: GPT-2-small block, 12 tensors" if args.step_api == "c1" else
+                                "C2: Llama-3.1-8B decoder layer, 9 tensors"), "params": n,
+                   "tensors": len(shapes)},
+        "results": res,
+    }), flush=True)
+
+
 def disk_bench(args):
     """The NVMe moment offload (LayerAdam(nvme_offload_fraction=1.0)) on this
     host: write and read back one C2 layer's exp_avg + exp_avg_sq (2 x 872 MB)
@@ -527,6 +608,9 @@ def main():
                          "c3 = the whole model, c3-layer = one of its decoder layers")
     ap.add_argument("--disk-bench", default=None, metavar="DIR",
                     help="instead of C2: time the moment file offload into DIR (host only)")
+    ap.add_argument("--step-api", choices=["c1", "c2"], default=None,
+                    help="instead of C2: time step(layer) / step_with_grad_views / per-tensor calls / step_chunk "
+                         "on one layer of separate tensors (prints its own JSON line)")
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
                     help="c2 (default, the headline): one Llama-3.1-8B layer; c3 / c4: whole resident "
                          "model / 48-layer stack (prints its own JSON line)")
@@ -551,6 +635,9 @@ def main():
         sys.exit(1)
     if args.streamed:
         streamed(args)
+        return
+    if args.step_api:
+        step_api(args)
         return
     if args.config != "c2":
         resident_stack(args)

@@ -424,16 +424,19 @@ def test_single_call_beyond_2_pow_31_elements(hip_device):
 # several calls of one step in one launch (la_adam_update_multi)
 # ---------------------------------------------------------------------------
 
-MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 2, 5000, 12, 129, 31, 8]
+# the last size is above the library's own-launch cut (16384 runs of 256 elements)
+MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 2, 5000, 12, 129, 31, 8,
+               16384 * 256 + 101]
 
 
 @pytest.mark.parametrize("triple", [("f32", "bf16", "f32"), ("f32", "f32", "f32"), ("bf16", "bf16", "bf16")])
 def test_multi_update_equals_separate_calls(triple, hip_device):
-    """20 segments (two launches of up to 16) of awkward sizes, some at odd
-    element offsets inside their buffers and one whose params are out of phase
-    with its grads (its own launch), with a clip coefficient and bf16 copies on
-    every other segment: bit-exact with the same 20 la_adam_update calls, and
-    every segment with the oracle replaying those calls."""
+    """21 segments of awkward sizes: 19 small ones (two batched launches of up
+    to 16), one large one above the own-launch cut and one whose params are out
+    of phase with its grads (both launched on their own).  Some sit at odd
+    element offsets inside their buffers; a clip coefficient applies and every
+    other segment writes a bf16 copy.  Bit-exact with the same 21
+    la_adam_update calls, and every segment with the oracle replaying them."""
     pk, gk, sk = triple
     td = {"f32": torch.float32, "bf16": torch.bfloat16}
     log(f"multi-update {triple}")
@@ -468,7 +471,7 @@ def test_multi_update_equals_separate_calls(triple, hip_device):
             assert np.array_equal(H.to_np_bits(sa[(0, 2, 3)[i]], kind), H.to_np_bits(sb[(0, 2, 3)[i]], kind)), (k, i)
         if sa[4] is not None:
             assert np.array_equal(H.to_np_bits(sa[4], "bf16"), H.to_np_bits(sb[4], "bf16")), k
-    # absolute check against the oracle, replaying the same 20 calls per step
+    # absolute check against the oracle, replaying the same 21 calls per step
     c = make()
     orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
     hp = [H.to_np_bits(s[0], pk) for s in c]
