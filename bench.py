@@ -158,6 +158,10 @@ def streamed(args):
         n, chunk, slots, lr, gstd = sum(LLAMA8B_LAYER), 16 * 1024 * 1024, 3, 1e-5, 1e-3
         workload = ("C3 layer: one Llama-3.1-8B-shaped layer (218,112,000 params) of the streamed model; "
                     "fp32 p/m/v in host RAM, 64 MB chunks x 3 slots; bf16 grads and bf16 copy in HBM")
+    if args.chunk_mi:
+        chunk = args.chunk_mi * 1024 * 1024
+    if args.slots:
+        slots = args.slots
     assert n % 16 == 0
     log(f"streamed {args.streamed}: n={n}, chunk={chunk}, slots={slots}")
     gen = torch.Generator(device=dev)
@@ -601,6 +605,10 @@ def main():
                     help="with --streamed: host state in pageable instead of pinned memory")
     ap.add_argument("--host-threads", type=int, default=0,
                     help="with --streamed: host threads that stage pageable arrays (0 = up to 16)")
+    ap.add_argument("--chunk-mi", type=int, default=0,
+                    help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
+    ap.add_argument("--slots", type=int, default=0,
+                    help="with --streamed c3-layer|c5: pipeline slots (default: the config's)")
     ap.add_argument("--no-staging", action="store_true",
                     help="with --streamed --pageable: leave pageable arrays to the HIP runtime's bounce buffers")
     ap.add_argument("--streamed", choices=["c5", "c3", "c3-layer"], default=None,

@@ -11,8 +11,51 @@
 #include <mutex>
 #include <thread>
 #include <vector>
+#if defined(__x86_64__)
+#include <emmintrin.h>
+#endif
 
 namespace la_host {
+
+// Copy `bytes` from src to dst.  The bulk goes through 16-byte nontemporal
+// stores (SSE2, part of every x86-64): the destination is written once and
+// not read back by this thread, so it should neither be read for ownership
+// nor evict the source from the caches.  Unaligned edges use memcpy.  Returns
+// true when nontemporal stores were issued (the caller then fences).
+#ifndef LA_COPY_NT
+#define LA_COPY_NT 1
+#endif
+
+inline bool copy_streaming(char* dst, const char* src, uint64_t bytes)
+{
+#if defined(__x86_64__) && LA_COPY_NT
+    const uint64_t head = (16u - (reinterpret_cast<uintptr_t>(dst) & 15u)) & 15u;
+    if (bytes < head + 256) {
+        std::memcpy(dst, src, bytes);
+        return false;
+    }
+    std::memcpy(dst, src, head);
+    dst += head;
+    src += head;
+    bytes -= head;
+    const uint64_t body = bytes & ~static_cast<uint64_t>(63);
+    for (uint64_t o = 0; o < body; o += 64) {
+        const __m128i a = _mm_loadu_si128(reinterpret_cast<const __m128i*>(src + o));
+        const __m128i b = _mm_loadu_si128(reinterpret_cast<const __m128i*>(src + o + 16));
+        const __m128i c = _mm_loadu_si128(reinterpret_cast<const __m128i*>(src + o + 32));
+        const __m128i d = _mm_loadu_si128(reinterpret_cast<const __m128i*>(src + o + 48));
+        _mm_stream_si128(reinterpret_cast<__m128i*>(dst + o), a);
+        _mm_stream_si128(reinterpret_cast<__m128i*>(dst + o + 16), b);
+        _mm_stream_si128(reinterpret_cast<__m128i*>(dst + o + 32), c);
+        _mm_stream_si128(reinterpret_cast<__m128i*>(dst + o + 48), d);
+    }
+    std::memcpy(dst + body, src + body, bytes - body);
+    return true;
+#else
+    std::memcpy(dst, src, bytes);
+    return false;
+#endif
+}
 
 struct Piece {
     char* dst;
@@ -71,11 +114,17 @@ private:
     }
     void drain(const std::vector<Piece>& pieces)
     {
+        bool streamed = false;
         for (;;) {
             const size_t i = next_.fetch_add(1);
-            if (i >= pieces.size()) return;
-            std::memcpy(pieces[i].dst, pieces[i].src, pieces[i].bytes);
+            if (i >= pieces.size()) break;
+            streamed |= copy_streaming(pieces[i].dst, pieces[i].src, pieces[i].bytes);
         }
+#if defined(__x86_64__)
+        // nontemporal stores are weakly ordered: make them globally visible
+        // before run() reports the copy done (the copy engines read them next)
+        if (streamed) _mm_sfence();
+#endif
     }
     void loop()
     {

@@ -11,7 +11,7 @@ beta-power state machine of the reference runs on the host inside that library.
 
 Device tensors are updated in place, asynchronously on the current HIP stream.
 Host tensors (the reference's layout: fp32 master and moments in CPU RAM) are
-streamed through HBM in 8 Mi-element chunks by the library's native
+streamed through HBM in 16 Mi-element chunks by the library's native
 three-stream pipeline (H2D / update / D2H overlapped) and the call returns
 after completion, as the reference's CPU call does; grads and the bf16 copy may
 then live on the host or on the device.  Pageable host arrays are copied
@@ -54,15 +54,17 @@ SUPPORTED_TRIPLES = frozenset({
     (torch.float32, torch.float16, torch.float32),
 })
 
-# Host tensors are streamed through HBM in chunks of this many elements (32 MB
+# Host tensors are streamed through HBM in chunks of this many elements (64 MB
 # of fp32 per state array), through HOST_STAGE_SLOTS staging slots.  A multiple
 # of 16, so that only the last chunk of a call holds the reference's scalar
 # tail (the last n % 16 elements of the call).  Measured on MI355X over one
-# Llama-3.1-8B layer of pinned state: 4-16 Mi-element chunks with 3-4 slots
-# all run at 46-47.5 GB/s each way (the concurrent-duplex limit of the host
-# link); larger chunks lose to pipeline fill and drain.
-HOST_STAGE_ELEMS = 8 * 1024 * 1024
-HOST_STAGE_SLOTS = 4
+# Llama-3.1-8B layer: with page-locked state, 4-16 Mi-element chunks with 3-4
+# slots all run at 46-47.5 GB/s each way (the concurrent-duplex limit of the
+# host link); with pageable state staged by host threads, 16 Mi x 3 runs at
+# 59-60 ms per layer every time while 8 Mi x 4 alternates between 59 and
+# 80-90 ms.
+HOST_STAGE_ELEMS = 16 * 1024 * 1024
+HOST_STAGE_SLOTS = 3
 
 
 class HostStreamer:
