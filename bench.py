@@ -181,20 +181,32 @@ def streamed(args):
     torch.cuda.synchronize()
     log(("pageable" if args.pageable else "pinned") + " state allocated and initialised")
 
-    adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, overlap_host_chunks=args.overlap)
     adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads,
                                         stage_pageable=not args.no_staging)
+    adam.add_layer_params(0, [torch.nn.Parameter(torch.empty(0))])  # a layer index for begin/end_chunk_step
     walls, host_copy = [], []
-    t = 0
+    call = args.call_chunk_mi * 1024 * 1024 if args.call_chunk_mi else n
     for i in range(args.warmup + args.steps):
-        t += 1
-        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=t), bf16_out=out)
-        st = adam.last_stream_stats
+        t0 = time.perf_counter()
+        wall_ms = copy_ms = 0.0
+        group = adam.begin_chunk_step(0)
+        for cs in range(0, n, call):
+            # the runtime's protocol: one step_chunk call per chunk (transformer_layer.py:470-476)
+            ce = min(n, cs + call)
+            adam.step_chunk(p[cs:ce], g[cs:ce], m[cs:ce], v[cs:ce], group, bf16_out=out[cs:ce])
+            st = adam.last_stream_stats
+            if st is not None:
+                wall_ms += st.wall_ms
+                copy_ms += st.host_copy_ms
+        adam.end_chunk_step(0)
+        if call < n or args.overlap:
+            wall_ms = (time.perf_counter() - t0) * 1e3      # host clock around all the calls
         if i >= args.warmup:
-            walls.append(st.wall_ms)
-            host_copy.append(st.host_copy_ms)
+            walls.append(wall_ms)
+            host_copy.append(copy_ms)
     wall = sum(walls) / len(walls)
-    h2d_bytes, d2h_bytes = st.h2d_bytes, st.d2h_bytes
+    h2d_bytes = d2h_bytes = 12 * n          # p, m, v each way; grads and the copy stay in HBM
 
     # isolated stages: the same copies alone, and the update alone on resident buffers
     stream = torch.cuda.current_stream(dev)
@@ -227,7 +239,8 @@ def streamed(args):
     t_d2h = timed(d2h_only)
     del dbuf
     pd, md, vd = (x.to(dev) for x in (p, m, v))
-    t_comp = timed(lambda: adam.step_chunk(pd, g, md, vd, dict(adam.defaults, step=t + 1), bf16_out=out))
+    t_comp = timed(lambda: adam.step_chunk(pd, g, md, vd, dict(adam.defaults, step=args.warmup + args.steps + 1),
+                                           bf16_out=out))
     del pd, md, vd
     res = {
         "metric": "streamed LayerAdam step (host-resident fp32 state), Gparams/s",
@@ -241,6 +254,7 @@ def streamed(args):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots,
+                   "elements_per_call": call, "overlap_host_chunks": bool(args.overlap),
                    "host_memory": "pageable" if args.pageable else "pinned",
                    "pageable_copies": ("none" if not args.pageable else
                                        "HIP runtime bounce buffers" if args.no_staging else
@@ -252,8 +266,8 @@ def streamed(args):
         "d2h_gbs_isolated": round(d2h_bytes / (t_d2h * 1e-3) / 1e9, 2),
         "isolated_ms": {"h2d": round(t_h2d, 3), "update": round(t_comp, 3), "d2h": round(t_d2h, 3)},
         "overlap": round((t_h2d + t_d2h + t_comp) / wall, 3),
-        "stream_spans_ms": {"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
-                            "d2h": round(st.d2h_ms, 3)},
+        "stream_spans_ms": ({"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
+                             "d2h": round(st.d2h_ms, 3)} if st is not None and call == n else None),
     }
     print(json.dumps(res), flush=True)
 
@@ -605,6 +619,11 @@ def main():
                     help="with --streamed: host state in pageable instead of pinned memory")
     ap.add_argument("--host-threads", type=int, default=0,
                     help="with --streamed: host threads that stage pageable arrays (0 = up to 16)")
+    ap.add_argument("--call-chunk-mi", type=int, default=0,
+                    help="with --streamed c3-layer|c5: split each step into step_chunk calls of this many Mi "
+                         "elements, as the runtime does (32); default: one call per step")
+    ap.add_argument("--overlap", action="store_true",
+                    help="with --streamed c3-layer|c5: LayerAdam(overlap_host_chunks=True)")
     ap.add_argument("--chunk-mi", type=int, default=0,
                     help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
     ap.add_argument("--slots", type=int, default=0,

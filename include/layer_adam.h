@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 3
+#define LA_ABI_VERSION 4
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -177,8 +177,17 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   g_on_host, else on the device; the bf16 copy `out` (nullable) goes to the
  *   host when out_on_host, else stays on the device.  Work queued on `after`
  *   before the call runs first; work queued on `after` later sees the
- *   result.  synchronize != 0 (or stats != NULL) waits for completion.
+ *   result.  synchronize != 0 (or stats != NULL) waits for completion of
+ *   this call and of every earlier one.  With synchronize == 0 the call
+ *   returns once its work is queued, and work queued on `after` later is not
+ *   ordered after it; its host arrays, device outputs, workspace and staging
+ *   must then stay valid, and must not be read or written by the caller,
+ *   until a synchronizing call or la_pipeline_sync.  The slot ring carries
+ *   over from call to call, so consecutive calls on disjoint host ranges
+ *   (the runtime's one call per chunk) keep both copy directions busy; a call
+ *   touching host bytes of an earlier unsettled call settles everything first.
  *   One pipeline object must not be used by two threads at once.
+ * la_pipeline_sync: wait until every queued call is complete in host memory.
  * la_pipeline_set_host_staging: attach caller-owned page-locked host memory
  *   (256-byte aligned, at least la_pipeline_workspace_bytes() for the call's
  *   types and placements) and the number of host copy threads (0 = up to 16),
@@ -186,8 +195,8 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   every pageable host array through it: `threads` host threads copy each
  *   chunk into the page-locked twin of its slot and the results back out, and
  *   the copy engines only ever see page-locked memory.  Without it pageable
- *   arrays go through the HIP runtime's own bounce buffers.  A call that
- *   stages returns after completion whatever `synchronize` says.  No
+ *   arrays go through the HIP runtime's own bounce buffers.  Changing the
+ *   attachment settles every queued call first.  No
  *   reference counterpart: the reference updates pageable state on the CPU.
  */
 typedef struct la_pipeline la_pipeline_t;
@@ -208,6 +217,7 @@ uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtyp
                                      int s_dtype, int g_on_host, int out_on_host);
 int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out);
 int la_pipeline_destroy(la_pipeline_t* pl);
+int la_pipeline_sync(la_pipeline_t* pl);
 int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads);
 int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host,
                      int g_dtype, const void* g, int g_on_host, int s_dtype, void* m_host,

@@ -40,6 +40,7 @@ EXPORTED = (
     "la_pipeline_workspace_bytes",
     "la_pipeline_create",
     "la_pipeline_destroy",
+    "la_pipeline_sync",
     "la_pipeline_set_host_staging",
     "la_pipeline_step",
     "la_disk_create",
@@ -139,6 +140,8 @@ def _declare(L):
     L.la_pipeline_create.restype = i
     L.la_pipeline_destroy.argtypes = [P]
     L.la_pipeline_destroy.restype = i
+    L.la_pipeline_sync.argtypes = [P]
+    L.la_pipeline_sync.restype = i
     L.la_pipeline_set_host_staging.argtypes = [P, P, u64, i]
     L.la_pipeline_set_host_staging.restype = i
     L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, i, P, P, u64, P, i, P, P, u64, P, i,

@@ -24,6 +24,13 @@
 // host threads copies chunk i of every pageable array into the twin, the copy
 // engines move the twin, and after the copy-back the threads copy the results
 // out of the twin before chunk i + S reuses it.
+//
+// Calls need not drain the pipeline.  The slot ring carries over from call to
+// call, so the runtime's one-call-per-chunk protocol (transformer_layer.py:
+// 470-476) keeps both copy directions busy across its calls.  A call with
+// synchronize == 0 returns once its work is queued; a staged chunk's copy-out
+// is then owed until its slot is reused, a call touches the same host bytes,
+// or la_pipeline_sync runs.
 
 #include <hip/hip_runtime.h>
 
@@ -54,6 +61,15 @@ struct la_pipeline {
     char* host_staging = nullptr;
     uint64_t host_staging_bytes = 0;
     std::unique_ptr<CopyPool> pool;
+    // the slot ring across calls: chunks issued so far; slot_used[s] once
+    // ev_d2h[s] has been recorded
+    uint64_t issued = 0;
+    std::vector<char> slot_used;
+    // copy-outs owed per slot (staged arrays of a chunk whose call returned
+    // before its results left the page-locked twin)
+    std::vector<std::vector<Piece>> owed;
+    // host byte ranges [lo, hi) touched by calls since the last full sync
+    std::vector<std::pair<uintptr_t, uintptr_t>> touched;
 };
 
 namespace {
@@ -111,14 +127,57 @@ void add_pieces(std::vector<Piece>& out, void* dst, const void* src, uint64_t by
         out.push_back(Piece{d + o, s + o, std::min(kPieceBytes, bytes - o)});
 }
 
+// Copy the results of slot s out of its page-locked twin once its copy-back
+// has landed (nothing to do when no copy-out is owed).
+int settle_slot(la_pipeline* pl, uint64_t s)
+{
+    if (pl->owed[s].empty()) return LA_OK;
+    const hipError_t e = hipEventSynchronize(pl->ev_d2h[s]);
+    if (e != hipSuccess) return rc_of(e);
+    pl->pool->run(pl->owed[s]);
+    pl->owed[s].clear();
+    return LA_OK;
+}
+
+// Everything queued so far has landed in host memory: owed copy-outs in slot
+// order of issue, then the copy streams.
+int settle_all(la_pipeline* pl)
+{
+    const uint64_t S = static_cast<uint64_t>(pl->slots);
+    for (uint64_t j = 0; j < S; ++j) {
+        const int rc = settle_slot(pl, (pl->issued + j) % S);
+        if (rc != LA_OK) return rc;
+    }
+    hipError_t e = hipStreamSynchronize(pl->h2d);
+    if (e == hipSuccess) e = hipStreamSynchronize(pl->comp);
+    if (e == hipSuccess) e = hipStreamSynchronize(pl->d2h);
+    pl->touched.clear();
+    return rc_of(e);
+}
+
 // After a failure part-way through a call, let the queued copies finish before
-// returning, so that nothing still writes the caller's memory afterwards.
+// returning, so that nothing still writes the caller's memory afterwards, and
+// deliver the copy-outs of every chunk whose copy-back was queued.
 int drain_streams(la_pipeline* pl, int rc)
 {
     (void)hipStreamSynchronize(pl->h2d);
     (void)hipStreamSynchronize(pl->comp);
     (void)hipStreamSynchronize(pl->d2h);
+    const uint64_t S = static_cast<uint64_t>(pl->slots);
+    for (uint64_t j = 0; j < S; ++j) {
+        std::vector<Piece>& o = pl->owed[(pl->issued + j) % S];
+        if (!o.empty() && pl->pool) pl->pool->run(o);
+        o.clear();
+    }
+    pl->touched.clear();
     return rc;
+}
+
+bool overlaps(const std::vector<std::pair<uintptr_t, uintptr_t>>& a, uintptr_t lo, uintptr_t hi)
+{
+    for (const auto& r : a)
+        if (lo < r.second && r.first < hi) return true;
+    return false;
 }
 
 void destroy_events(la_pipeline* pl)
@@ -153,6 +212,8 @@ int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out)
     if (!pl) return LA_EINVAL;
     pl->chunk = chunk_elems;
     pl->slots = slots;
+    pl->slot_used.assign(static_cast<size_t>(slots), 0);
+    pl->owed.resize(static_cast<size_t>(slots));
     hipError_t e = hipGetDevice(&pl->device);
     // default priority everywhere (hipStreamCreateWithFlags, no priority argument)
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&pl->h2d, hipStreamNonBlocking);
@@ -180,6 +241,8 @@ int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out)
 int la_pipeline_destroy(la_pipeline_t* pl)
 {
     if (!pl) return LA_OK;
+    // copy-outs still owed are completed: the host arrays must still be valid
+    if (pl->pool && pl->h2d && pl->comp && pl->d2h) (void)settle_all(pl);
     if (pl->h2d) (void)hipStreamSynchronize(pl->h2d);
     if (pl->comp) (void)hipStreamSynchronize(pl->comp);
     if (pl->d2h) (void)hipStreamSynchronize(pl->d2h);
@@ -191,9 +254,24 @@ int la_pipeline_destroy(la_pipeline_t* pl)
     return LA_OK;
 }
 
+int la_pipeline_sync(la_pipeline_t* pl)
+{
+    if (!pl) return LA_EINVAL;
+    return settle_all(pl);
+}
+
 int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads)
 {
     if (!pl) return LA_EINVAL;
+    if (threads == 0) threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
+    if (static_cast<char*>(pinned) == pl->host_staging && (!pinned || (bytes == pl->host_staging_bytes && pl->pool &&
+                                                                       pl->pool->threads() == threads)))
+        return LA_OK;  // unchanged
+    // owed copy-outs read the current twins: settle them before the staging changes
+    {
+        const int rc = settle_all(pl);
+        if (rc != LA_OK) return rc;
+    }
     if (!pinned) {
         pl->host_staging = nullptr;
         pl->host_staging_bytes = 0;
@@ -202,7 +280,6 @@ int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes
     if (bytes == 0 || reinterpret_cast<uintptr_t>(pinned) % kAlign || threads < 0 || threads > 64) return LA_EINVAL;
     char* base = static_cast<char*>(pinned);
     if (!page_locked(base) || !page_locked(base + bytes - 1)) return LA_EINVAL;
-    if (threads == 0) threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
     if (!pl->pool || pl->pool->threads() != threads) {
         pl->pool.reset();
         try {
@@ -271,6 +348,28 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     double host_copy_ms = 0.0;
     std::vector<Piece> pieces;
 
+    // Host bytes this call reads or writes.  If an earlier call that has not
+    // been settled touched any of them (the same layer stepped again), settle
+    // everything first; otherwise this call streams on behind the earlier ones.
+    std::pair<uintptr_t, uintptr_t> ranges[5];
+    int nranges = 0;
+    auto add_range = [&](const void* ptr, uint64_t bytes) {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr);
+        ranges[nranges++] = {lo, lo + bytes};
+    };
+    add_range(ph, n * pb);
+    add_range(mh, n * sb);
+    add_range(vh, n * sb);
+    if (g_on_host) add_range(gp, n * gb);
+    if (out && out_on_host) add_range(op, n * 2);
+    bool clash = pl->touched.size() > 4096;
+    for (int r = 0; r < nranges && !clash; ++r) clash = overlaps(pl->touched, ranges[r].first, ranges[r].second);
+    if (clash) {
+        const int rc = settle_all(pl);
+        if (rc != LA_OK) return rc;
+    }
+    for (int r = 0; r < nranges; ++r) pl->touched.push_back(ranges[r]);
+
     auto host_copy = [&]() {
         const auto a = std::chrono::steady_clock::now();
         pl->pool->run(pieces);
@@ -278,17 +377,12 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
         for (const Piece& q : pieces) staged_bytes += q.bytes;
         pieces.clear();
     };
-    // results of chunk j leave the page-locked twin of its slot (staged arrays only)
-    auto copy_out = [&](uint64_t j) -> int {
-        const uint64_t s = j % S, off = j * pl->chunk;
-        const uint64_t k = (n - off) < pl->chunk ? (n - off) : pl->chunk;
-        char* hs = pl->host_staging + s * L.slot_bytes;
+    // settle a slot's owed copy-out, counting it in this call's statistics
+    auto settle = [&](uint64_t s) -> int {
+        if (pl->owed[s].empty()) return LA_OK;
         const hipError_t e = hipEventSynchronize(pl->ev_d2h[s]);
         if (e != hipSuccess) return rc_of(e);
-        if (st_p) add_pieces(pieces, ph + off * pb, hs + L.p, k * pb);
-        if (st_m) add_pieces(pieces, mh + off * sb, hs + L.m, k * sb);
-        if (st_v) add_pieces(pieces, vh + off * sb, hs + L.v, k * sb);
-        if (st_o) add_pieces(pieces, op + off * 2, hs + L.out, k * 2);
+        pieces.swap(pl->owed[s]);
         host_copy();
         return LA_OK;
     };
@@ -299,8 +393,6 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
         if (e_ != hipSuccess) return drain_streams(pl, rc_of(e_)); \
     } while (0)
 
-    // the slots are free once the previous call's last copy-back is done
-    LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->t_end, 0));
     // everything the caller queued before (e.g. the backward that produced g) comes first
     LA_STEP_TRY(hipEventRecord(pl->t_begin, caller));
     LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->t_begin, 0));
@@ -308,31 +400,28 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     LA_STEP_TRY(hipStreamWaitEvent(pl->d2h, pl->t_begin, 0));
     LA_STEP_TRY(hipEventRecord(pl->t_comp_begin, pl->comp));
     LA_STEP_TRY(hipEventRecord(pl->t_d2h_begin, pl->d2h));
-    // host threads read the host arrays directly: the caller's queued work and the
-    // previous call's copy-backs must be complete before they do
-    if (staged) {
-        LA_STEP_TRY(hipEventSynchronize(pl->t_begin));
-        LA_STEP_TRY(hipStreamSynchronize(pl->d2h));
-    }
+    // host threads read the host arrays directly: the caller's queued work must be done first
+    if (staged) LA_STEP_TRY(hipEventSynchronize(pl->t_begin));
 
     for (uint64_t i = 0; i < nchunks; ++i) {
-        const uint64_t s = i % S;
+        const uint64_t s = pl->issued % S;
         const uint64_t off = i * pl->chunk;
         const uint64_t k = (n - off) < pl->chunk ? (n - off) : pl->chunk;
         char* slot = ws + s * L.slot_bytes;
         char* hs = staged ? pl->host_staging + s * L.slot_bytes : nullptr;
+        {
+            // the twin of slot s still holds the results of chunk issued - S
+            const int rc = settle(s);
+            if (rc != LA_OK) return drain_streams(pl, rc);
+        }
         if (staged) {
-            if (i >= S) {
-                const int rc = copy_out(i - S);
-                if (rc != LA_OK) return drain_streams(pl, rc);
-            }
             if (st_p) add_pieces(pieces, hs + L.p, ph + off * pb, k * pb);
             if (st_m) add_pieces(pieces, hs + L.m, mh + off * sb, k * sb);
             if (st_v) add_pieces(pieces, hs + L.v, vh + off * sb, k * sb);
             if (st_g) add_pieces(pieces, hs + L.g, gp + off * gb, k * gb);
             host_copy();
         }
-        if (i >= S) LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->ev_d2h[s], 0));
+        if (pl->slot_used[s]) LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->ev_d2h[s], 0));
         LA_STEP_TRY(hipMemcpyAsync(slot + L.p, st_p ? hs + L.p : ph + off * pb, k * pb, hipMemcpyHostToDevice,
                                    pl->h2d));
         LA_STEP_TRY(hipMemcpyAsync(slot + L.m, st_m ? hs + L.m : mh + off * sb, k * sb, hipMemcpyHostToDevice,
@@ -371,23 +460,33 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
             d2h_bytes += k * 2;
         }
         LA_STEP_TRY(hipEventRecord(pl->ev_d2h[s], pl->d2h));
+        pl->slot_used[s] = 1;
+        pl->issued++;
+        // the results of staged arrays are owed until they leave the twin
+        if (st_p) add_pieces(pl->owed[s], ph + off * pb, hs + L.p, k * pb);
+        if (st_m) add_pieces(pl->owed[s], mh + off * sb, hs + L.m, k * sb);
+        if (st_v) add_pieces(pl->owed[s], vh + off * sb, hs + L.v, k * sb);
+        if (st_o) add_pieces(pl->owed[s], op + off * 2, hs + L.out, k * 2);
     }
     LA_STEP_TRY(hipEventRecord(pl->t_h2d_end, pl->h2d));
     LA_STEP_TRY(hipEventRecord(pl->t_comp_end, pl->comp));
     LA_STEP_TRY(hipEventRecord(pl->t_end, pl->d2h));
-    // later work on the caller's stream sees the updated state
-    LA_STEP_TRY(hipStreamWaitEvent(caller, pl->t_end, 0));
-    if (staged) {
-        // the last S chunks still sit in their page-locked twins
-        for (uint64_t j = nchunks > S ? nchunks - S : 0; j < nchunks; ++j) {
-            const int rc = copy_out(j);
-            if (rc != LA_OK) return drain_streams(pl, rc);
-        }
-    }
+    // later work on the caller's stream sees the updated state.  Not for a call
+    // that returns once queued: the next call records its start on the caller's
+    // stream, and that wait would make it start only after this call's last
+    // copy-back; such calls are completed by la_pipeline_sync instead.
+    if (synchronize || stats) LA_STEP_TRY(hipStreamWaitEvent(caller, pl->t_end, 0));
 #undef LA_STEP_TRY
     if (synchronize || stats) {
+        // every copy-out owed, this call's and earlier ones, in order of issue
+        for (uint64_t j = 0; j < S; ++j) {
+            const int rc = settle((pl->issued + j) % S);
+            if (rc != LA_OK) return drain_streams(pl, rc);
+        }
         const hipError_t e = hipEventSynchronize(pl->t_end);
         if (e != hipSuccess) return rc_of(e);
+        // t_end follows every earlier call's copy-backs on the same stream
+        pl->touched.clear();
     }
     if (stats) {
         stats->h2d_bytes = h2d_bytes;

@@ -120,7 +120,9 @@ class HostStreamer:
                    "la_pipeline_set_host_staging")
 
     def step(self, scalars, pc, params, gc, grads, g_on_host, sc, exp_avg, exp_avg_sq, n, bf16_out,
-             out_on_host, clip_coef, stream_handle):
+             out_on_host, clip_coef, stream_handle, synchronize: bool = True):
+        """One la_pipeline_step.  With synchronize=False it returns once the work
+        is queued (statistics then None); ``sync()`` completes it."""
         key = (pc, gc, sc, g_on_host, out_on_host)
         ws = self.workspace(*key)
         host = [params, exp_avg, exp_avg_sq] + ([grads] if g_on_host else []) + \
@@ -128,15 +130,20 @@ class HostStreamer:
         self._attach_host_staging(key, self.stage_pageable and not all(t.is_pinned() for t in host))
         base = ws.data_ptr()
         aligned = (base + 255) // 256 * 256
-        stats = _lib.LaPipelineStats()
+        stats = _lib.LaPipelineStats() if synchronize else None
         rc = self.lib.la_pipeline_step(
             self.handle, ctypes.byref(scalars), pc, params.data_ptr(), gc, grads.data_ptr(),
             int(g_on_host), sc, exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n,
             None if bf16_out is None else bf16_out.data_ptr(), int(out_on_host),
             None if clip_coef is None else clip_coef.data_ptr(), aligned,
-            ws.numel() - (aligned - base), stream_handle, 1, ctypes.byref(stats))
+            ws.numel() - (aligned - base), stream_handle, int(synchronize),
+            None if stats is None else ctypes.byref(stats))
         _lib.check(rc, "la_pipeline_step")
         return stats
+
+    def sync(self):
+        """Wait until every queued step is complete in host memory."""
+        _lib.check(self.lib.la_pipeline_sync(self.handle), "la_pipeline_sync")
 
     def __del__(self):
         try:
@@ -236,12 +243,18 @@ class LayerAdam:
             *,
             device: Optional[torch.device] = None,
             pin_host_state: bool = False,
+            overlap_host_chunks: bool = False,
     ):
         """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
         ``device``: the HIP device that updates host-resident state (default: current);
         ``pin_host_state``: allocate host-resident moments in page-locked memory
         (streamed without staging copies; the reference allocates pageable memory,
-        which the pipeline stages through page-locked buffers)."""
+        which the pipeline stages through page-locked buffers);
+        ``overlap_host_chunks``: host-tensor updates return once queued, so that
+        the runtime's one ``step_chunk`` per chunk keeps the host link busy across
+        calls; ``end_chunk_step``, the end of ``step``/``step_with_grad_views`` and
+        ``synchronize()`` complete them.  Between those points the host tensors
+        passed in must not be read, written or freed."""
         self.defaults = dict(
             lr=lr,
             bias_correction=bias_correction,
@@ -266,6 +279,7 @@ class LayerAdam:
         self.num_layer = num_layer
         self.device = torch.device(device) if device is not None else None
         self.pin_host_state = pin_host_state
+        self.overlap_host_chunks = overlap_host_chunks
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
         assert 0.0 <= nvme_offload_fraction <= 1.0
@@ -505,7 +519,8 @@ class LayerAdam:
             out_on_host = bf16_out is not None and not bf16_out.is_cuda
             self.last_stream_stats = streamer.step(
                 sc, pc, params, gc, grads, g_on_host, sc_, exp_avg, exp_avg_sq, n, bf16_out,
-                out_on_host, clip_coef, _stream_handle(stream, device))
+                out_on_host, clip_coef, _stream_handle(stream, device),
+                synchronize=not self.overlap_host_chunks)
 
     # ------------------------------------------------------------------
     # steps (layer_adam.py:270-468)
@@ -533,6 +548,7 @@ class LayerAdam:
                 assert p.data.numel() == p.grad.data.numel(), "params and grads must have the same size"
                 entries.append((p.data, p.grad.data, state['exp_avg'], state['exp_avg_sq']))
             self._update_tensors(param_group, entries)
+        self.synchronize()
         self._post_step(layer_idx)
         return loss
 
@@ -562,8 +578,17 @@ class LayerAdam:
                 assert p.data.numel() == grad.numel(), "params and grads must have the same size"
                 entries.append((p.data, grad, state['exp_avg'], state['exp_avg_sq']))
             self._update_tensors(param_group, entries)
+        self.synchronize()
         self._post_step(layer_idx)
         return loss
+
+    def synchronize(self):
+        """Complete every host-tensor update still in flight (they are only in
+        flight with ``overlap_host_chunks=True``)."""
+        if self.overlap_host_chunks:
+            for streamer in self._streamers.values():
+                with torch.cuda.device(streamer.device):
+                    streamer.sync()
 
     def _update_tensors(self, param_group, entries):
         """The per-tensor adam_update calls of step(layer) / step_with_grad_views
@@ -609,7 +634,9 @@ class LayerAdam:
         ``bf16_out``: optional bf16 tensor receiving the compute copy of the
         updated params.  ``clip_coef``: optional device fp32 scalar multiplying
         the grads (see ``clip_grad_norm``).  Device tensors: asynchronous on
-        ``stream`` (default: current stream).  Host tensors: returns after completion.
+        ``stream`` (default: current stream).  Host tensors: returns after
+        completion, or, with ``overlap_host_chunks=True``, once queued
+        (``end_chunk_step`` completes the chunks).
         """
         self.adam_update(param_group['step'], param_group['lr'], param_group['betas'][0],
                          param_group['betas'][1], param_group['eps'], param_group['weight_decay'],
@@ -618,7 +645,8 @@ class LayerAdam:
 
     @torch.no_grad()
     def end_chunk_step(self, layer_idx: int):
-        """End a chunked step: NVMe write-back (layer_adam.py:464-468)."""
+        """End a chunked step: every chunk complete, then NVMe write-back (layer_adam.py:464-468)."""
+        self.synchronize()
         self._post_step(layer_idx)
 
     def update_learning_rate(self, new_lr):

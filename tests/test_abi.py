@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
-    assert L.la_abi_version() == version == 3
+    assert L.la_abi_version() == version == 4
 
 
 def test_library_is_gfx950_code_object():

@@ -425,6 +425,60 @@ def test_pageable_state_staged_through_page_locked_twins(pinned_p, g_host, out_h
     assert np.array_equal(results[0][3], O.f32_to_bf16(ph))
 
 
+@pytest.mark.parametrize("pinned", [True, False])
+def test_overlapped_host_chunks_in_the_runtime_protocol(pinned, hip_device):
+    """LayerAdam(overlap_host_chunks=True) in the runtime's protocol on host
+    state (transformer_layer.py:453-493): begin_chunk_step, one step_chunk per
+    5000-element chunk with host grads, end_chunk_step.  The step_chunk calls
+    return once queued and stream on behind each other through a 2048-element
+    pipeline of 3 slots; end_chunk_step completes them.  Then two steps are
+    queued back to back on the same bytes without end_chunk_step in between,
+    which makes the second call settle the first.  Bit-exact with the oracle
+    after every step, page-locked (no staging) and pageable (staged) state."""
+    from slideformer_amd.layer_adam import HostStreamer
+    n, call = 23_456, 5000
+    rng = np.random.default_rng(60 + int(pinned))
+    p0 = rng.normal(0, 0.02, n).astype(np.float32)
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, pin_host_state=pinned, overlap_host_chunks=True)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=2048, slots=3)
+    master = torch.from_numpy(p0.copy())
+    if pinned:
+        master = master.pin_memory()
+    adam.add_layer_params(0, [torch.nn.Parameter(master)])
+    m, v = adam.exp_avg_flat[0], adam.exp_avg_sq_flat[0]
+    assert m.is_pinned() == pinned and master.is_pinned() == pinned
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    ph, mh, vh = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+
+    def check():
+        assert np.array_equal(master.numpy().view(np.uint32), ph.view(np.uint32))
+        assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
+        assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
+
+    for _ in range(3):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16().pin_memory()
+        gb = H.to_np_bits(g, "bf16")
+        group = adam.begin_chunk_step(0)
+        for cs in range(0, n, call):
+            ce = min(n, cs + call)
+            adam.step_chunk(master[cs:ce], g[cs:ce], m[cs:ce], v[cs:ce], group)
+            assert adam.last_stream_stats is None          # returned once queued
+            orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[cs:ce], gb[cs:ce], mh[cs:ce],
+                       vh[cs:ce], g16="bf16")
+        adam.end_chunk_step(0)
+        check()
+    # two whole-buffer steps queued back to back: the second call touches the
+    # first one's bytes and settles it before streaming
+    gs = [torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16().pin_memory() for _ in range(2)]
+    for g in gs:
+        group = adam.begin_chunk_step(0)
+        adam.step_chunk(master, g, m, v, group)
+        orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh,
+                   g16="bf16")
+    adam.synchronize()
+    check()
+
+
 def test_host_staging_rejects_bad_buffers(hip_device):
     """la_pipeline_set_host_staging accepts only 256-byte aligned page-locked
     memory; a staging buffer smaller than a call needs fails the call before any
