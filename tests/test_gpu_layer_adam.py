@@ -479,6 +479,46 @@ def test_overlapped_host_chunks_in_the_runtime_protocol(pinned, hip_device):
     check()
 
 
+@pytest.mark.parametrize("triple", [("bf16", "bf16", "bf16"), ("f16", "f32", "f32"), ("f16", "f16", "f16")])
+def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
+    """The streaming pipeline on the reference's other dtype triples: 16-bit
+    params and states, host grads and a host bf16 copy, all pageable (staged),
+    overlapped calls of 3000 elements through 1024-element chunks in 2 slots.
+    Bit-exact with the oracle."""
+    from slideformer_amd.layer_adam import HostStreamer
+    pk, gk, sk = triple
+    td = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+    k16 = {"f32": None, "bf16": "bf16", "f16": "f16"}
+    n, call = 10_007, 3000
+    rng = np.random.default_rng(70)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(td[pk])
+    m = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(td[sk])
+    v = torch.from_numpy(np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)).to(td[sk])
+    out = torch.empty(n, dtype=torch.bfloat16)
+    bits = lambda t, k: H.to_np_bits(t, k)
+    hp, hm, hv = bits(p, pk), bits(m, sk), bits(v, sk)
+    view = lambda b, k: b.view(np.float32) if k == "f32" else b
+    ho = np.zeros(n, np.uint16)                      # the oracle's bf16 copy: RNE of the fp32 result
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, overlap_host_chunks=True)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=1024, slots=2, host_threads=2)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(td[gk])
+        gb = bits(g, gk)
+        group = dict(adam.defaults, step=step)
+        for cs in range(0, n, call):
+            ce = min(n, cs + call)
+            adam.step_chunk(p[cs:ce], g[cs:ce], m[cs:ce], v[cs:ce], group, bf16_out=out[cs:ce])
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, view(hp, pk)[cs:ce], view(gb, gk)[cs:ce],
+                       view(hm, sk)[cs:ce], view(hv, sk)[cs:ce], p16=k16[pk], g16=k16[gk], s16=k16[sk],
+                       p_bf16_out=ho[cs:ce])
+        adam.synchronize()
+    assert np.array_equal(bits(p, pk), hp)
+    assert np.array_equal(bits(m, sk), hm)
+    assert np.array_equal(bits(v, sk), hv)
+    assert np.array_equal(H.to_np_bits(out, "bf16"), ho)
+
+
 def test_host_staging_rejects_bad_buffers(hip_device):
     """la_pipeline_set_host_staging accepts only 256-byte aligned page-locked
     memory; a staging buffer smaller than a call needs fails the call before any
