@@ -429,8 +429,9 @@ MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 
                16384 * 256 + 101]
 
 
+@pytest.mark.parametrize("mode", ["adamw", "l2", "none"])
 @pytest.mark.parametrize("triple", [("f32", "bf16", "f32"), ("f32", "f32", "f32"), ("bf16", "bf16", "bf16")])
-def test_multi_update_equals_separate_calls(triple, hip_device):
+def test_multi_update_equals_separate_calls(triple, mode, hip_device):
     """21 segments of awkward sizes: 19 small ones (two batched launches of up
     to 16), one large one above the own-launch cut and one whose params are out
     of phase with its grads (both launched on their own).  Some sit at odd
@@ -439,7 +440,9 @@ def test_multi_update_equals_separate_calls(triple, hip_device):
     la_adam_update calls, and every segment with the oracle replaying them."""
     pk, gk, sk = triple
     td = {"f32": torch.float32, "bf16": torch.bfloat16}
-    log(f"multi-update {triple}")
+    log(f"multi-update {triple} {mode}")
+    wd = 0.0 if mode == "none" else 0.01
+    adamw = mode != "l2"
     coef = torch.tensor([0.37], device=hip_device)
 
     def make():
@@ -459,12 +462,12 @@ def test_multi_update_equals_separate_calls(triple, hip_device):
         return segs
 
     a, b = make(), make()
-    opt_a = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
-    opt_b = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    opt_a = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, wd, adamw)
+    opt_b = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, wd, adamw)
     for step in (1, 2, 3):
-        opt_a.update_multi(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, a, coef=coef)
+        opt_a.update_multi(step, 1e-3, 0.9, 0.999, 1e-8, wd, True, a, coef=coef)
         for p, g, m, v, out in b:
-            opt_b.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, out=out, coef=coef)
+            opt_b.update(step, 1e-3, 0.9, 0.999, 1e-8, wd, True, p, g, m, v, out=out, coef=coef)
     torch.cuda.synchronize()
     for k, (sa, sb) in enumerate(zip(a, b)):
         for i, kind in enumerate((pk, sk, sk)):
@@ -473,14 +476,14 @@ def test_multi_update_equals_separate_calls(triple, hip_device):
             assert np.array_equal(H.to_np_bits(sa[4], "bf16"), H.to_np_bits(sb[4], "bf16")), k
     # absolute check against the oracle, replaying the same 21 calls per step
     c = make()
-    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, wd, adamw)
     hp = [H.to_np_bits(s[0], pk) for s in c]
     hm = [H.to_np_bits(s[2], sk) for s in c]
     hv = [H.to_np_bits(s[3], sk) for s in c]
     hg = [H.to_np_bits(s[1], gk) for s in c]
     for step in (1, 2, 3):
         for k in range(len(c)):
-            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, _view(hp[k], pk), _view(hg[k], gk),
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, wd, True, _view(hp[k], pk), _view(hg[k], gk),
                        _view(hm[k], sk), _view(hv[k], sk), p16=KIND16[pk], g16=KIND16[gk], s16=KIND16[sk],
                        clip_coef=0.37)
     for k in range(len(c)):
