@@ -306,6 +306,13 @@ class LayerAdam:
             self.offloader = None
 
     def __del__(self):
+        # overlapped host updates still write exp_avg / exp_avg_sq: finish them
+        # while those buffers are certainly alive
+        try:
+            if getattr(self, '_streamers', None):
+                self.synchronize()
+        except Exception:
+            pass
         if hasattr(self, 'lib') and hasattr(self, 'optimizer_id'):
             try:
                 self.lib.la_destroy(self.optimizer_id)
