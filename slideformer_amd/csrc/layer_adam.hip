@@ -21,7 +21,7 @@
 // (cpu_adam_impl.cpp:46-67) as its GCC build contracts it.
 //
 // The grad norm is two launches: stage 1 keeps per-lane float64 sums, reduces
-// them across the wave64 with DPP and across the 4 waves of a workgroup in
+// them across the wave64 with DPP and across the 8 waves of a workgroup in
 // LDS, and writes one partial per workgroup to the caller's workspace; stage 2
 // (one workgroup) folds the partials in a fixed order and, optionally, writes
 // the clip coefficient.
@@ -46,24 +46,26 @@
 #ifndef LA_BLOCK
 #define LA_BLOCK 64
 #endif
-// Grad-norm workgroup size (4 waves; partials are folded in LDS first).
+// Grad-norm workgroup size (8 waves; partials are folded in LDS first).
 #ifndef LA_NORM_BLOCK
-#define LA_NORM_BLOCK 256
+#define LA_NORM_BLOCK 512
 #endif
 // Upper bound on update workgroups per launch (grid-stride beyond it).
 #ifndef LA_MAX_GRID
 #define LA_MAX_GRID (1 << 26)
 #endif
 // Upper bound on grad-norm stage-1 workgroups (= partials folded by stage 2).
-// Measured on MI355X over a 218M-element bf16 buffer: 1024 workgroups with 4
-// groups per lane per trip read at ~6.5 TB/s (67 us), 2048 x 2 at ~6.2 TB/s
-// (70 us); larger grids lose to the single-workgroup fold.
+// Measured on MI355X over a 218M-element bf16 buffer (workgroup size x
+// workgroups x groups of 4 per lane per trip): 512 x 256 x 8 reads in
+// 62.5-62.7 us (7.0 TB/s, 87 %), 256 x 512 x 8 in 63-64, 256 x 256 x 16 in
+// 63, 256 x 1024 x 4 in 67-68, 256 x 2048 x 2 in 70, 256 x 2048 x 4 in 83.
+// About 8 waves per CU, each with 4 KB in flight per trip, read best.
 #ifndef LA_NORM_MAX_GRID
-#define LA_NORM_MAX_GRID 1024
+#define LA_NORM_MAX_GRID 256
 #endif
 // Groups of 4 each lane of the grad-norm kernel loads per loop trip.
 #ifndef LA_NORM_UNROLL
-#define LA_NORM_UNROLL 4
+#define LA_NORM_UNROLL 8
 #endif
 // Nontemporal hints on the streaming loads / stores.
 #ifndef LA_NT_LOAD
