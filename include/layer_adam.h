@@ -185,7 +185,9 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   until a synchronizing call or la_pipeline_sync.  The slot ring carries
  *   over from call to call, so consecutive calls on disjoint host ranges
  *   (the runtime's one call per chunk) keep both copy directions busy; a call
- *   touching host bytes of an earlier unsettled call settles everything first.
+ *   touching host bytes of an earlier unsettled call, or using another
+ *   workspace or slot layout (element types, g/out placement) than the
+ *   previous call, settles everything first.
  *   One pipeline object must not be used by two threads at once.
  * la_pipeline_sync: wait until every queued call is complete in host memory.
  * la_pipeline_set_host_staging: attach caller-owned page-locked host memory

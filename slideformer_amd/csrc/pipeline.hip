@@ -70,6 +70,10 @@ struct la_pipeline {
     std::vector<std::vector<Piece>> owed;
     // host byte ranges [lo, hi) touched by calls since the last full sync
     std::vector<std::pair<uintptr_t, uintptr_t>> touched;
+    // device workspace and slot size of the last call: slot s of another
+    // layout can overlap slot s + 1 of this one
+    const char* last_ws = nullptr;
+    uint64_t last_slot_bytes = 0;
 };
 
 namespace {
@@ -363,12 +367,17 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
     if (g_on_host) add_range(gp, n * gb);
     if (out && out_on_host) add_range(op, n * 2);
     bool clash = pl->touched.size() > 4096;
+    // another workspace or slot layout than the previous call's: the slots of
+    // the two layouts overlap, so earlier work must be finished first
+    if (pl->issued > 0 && (ws != pl->last_ws || L.slot_bytes != pl->last_slot_bytes)) clash = true;
     for (int r = 0; r < nranges && !clash; ++r) clash = overlaps(pl->touched, ranges[r].first, ranges[r].second);
     if (clash) {
         const int rc = settle_all(pl);
         if (rc != LA_OK) return rc;
     }
     for (int r = 0; r < nranges; ++r) pl->touched.push_back(ranges[r]);
+    pl->last_ws = ws;
+    pl->last_slot_bytes = L.slot_bytes;
 
     auto host_copy = [&]() {
         const auto a = std::chrono::steady_clock::now();

@@ -519,6 +519,63 @@ def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
     assert np.array_equal(H.to_np_bits(out, "bf16"), ho)
 
 
+def test_async_pipeline_calls_with_changing_layouts(hip_device):
+    """Raw la_pipeline_step calls with synchronize = 0 on disjoint ranges of
+    pageable host state, one workspace and one staging buffer for all, but
+    alternating slot layouts (grads on the device / on the host, fp32 / bf16
+    grads): each layout change settles the earlier calls, whose slots would
+    otherwise overlap the new ones.  la_pipeline_sync completes the last.
+    Bit-exact with the oracle."""
+    import ctypes
+
+    from slideformer_amd import _lib
+    from slideformer_amd.layer_adam import HostStreamer
+
+    L = _lib.load()
+    chunk, slots, n, part = 1024, 3, 6 * 2600, 2600
+    s_ = HostStreamer(hip_device, chunk_elems=chunk, slots=slots)
+    F32, BF16 = _lib.LA_F32, _lib.LA_BF16
+    need = max(L.la_pipeline_workspace_bytes(chunk, slots, F32, gc, F32, gh, 0)
+               for gc in (F32, BF16) for gh in (0, 1))
+    ws = torch.empty(need + 256, dtype=torch.uint8, device=hip_device)
+    wbase = (ws.data_ptr() + 255) // 256 * 256
+    stg = torch.empty(need + 256, dtype=torch.uint8, pin_memory=True)
+    sbase = (stg.data_ptr() + 255) // 256 * 256
+    assert L.la_pipeline_set_host_staging(s_.handle, sbase, need, 2) == 0
+    rng = np.random.default_rng(80)
+    p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32))
+    m, v = torch.zeros(n), torch.zeros(n)
+    ph, mh, vh = p.numpy().copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    L.la_create(81, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    st = torch.cuda.current_stream(hip_device).cuda_stream
+    layouts = [(BF16, False), (F32, True), (BF16, True), (F32, False), (BF16, False), (F32, True)]
+    keep = []
+    for i, (gc, on_host) in enumerate(layouts):
+        lo, hi = i * part, (i + 1) * part
+        g32 = rng.normal(0, 1e-3, part).astype(np.float32)
+        g = torch.from_numpy(g32)
+        if gc == BF16:
+            g = g.bfloat16()
+        gbits = H.to_np_bits(g, "bf16" if gc == BF16 else "f32")
+        if not on_host:
+            g = g.to(hip_device)
+        keep.append(g)
+        sc = _lib.LaScalars()
+        assert L.la_scalars(81, 1, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, ctypes.byref(sc)) == 0
+        rc = L.la_pipeline_step(s_.handle, ctypes.byref(sc), F32, p[lo:hi].data_ptr(), gc, g.data_ptr(),
+                                int(on_host), F32, m[lo:hi].data_ptr(), v[lo:hi].data_ptr(), hi - lo, None, 0,
+                                None, wbase, need, st, 0, None)
+        assert rc == 0, rc
+        orc.update(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[lo:hi], g32 if gc == F32 else gbits, mh[lo:hi],
+                   vh[lo:hi], g16="bf16" if gc == BF16 else None)
+    assert L.la_pipeline_sync(s_.handle) == 0
+    assert np.array_equal(p.numpy().view(np.uint32), ph.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), mh.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), vh.view(np.uint32))
+    L.la_destroy(81)
+
+
 def test_host_staging_rejects_bad_buffers(hip_device):
     """la_pipeline_set_host_staging accepts only 256-byte aligned page-locked
     memory; a staging buffer smaller than a call needs fails the call before any
