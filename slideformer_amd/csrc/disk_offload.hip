@@ -143,7 +143,19 @@ int la_disk_create(const char* dir, int threads, la_disk_t** out)
     la_disk* d = new (std::nothrow) la_disk();
     if (!d) return -ENOMEM;
     d->dir = dir;
-    for (int i = 0; i < threads; ++i) d->workers.emplace_back(worker_loop, d);
+    try {
+        for (int i = 0; i < threads; ++i) d->workers.emplace_back(worker_loop, d);
+    } catch (...) {
+        // no exception crosses the C ABI: stop the workers already started
+        {
+            std::lock_guard<std::mutex> lk(d->mu);
+            d->stop = true;
+        }
+        d->work_cv.notify_all();
+        for (auto& t : d->workers) t.join();
+        delete d;
+        return -EAGAIN;
+    }
     *out = d;
     return LA_OK;
 }
