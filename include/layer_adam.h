@@ -8,7 +8,9 @@
  *
  * Return codes: 0 on success; LA_EINVAL for a null/misaligned pointer, an
  * unknown id or a bad size; LA_EDTYPE for a dtype triple the reference does
- * not register; a positive hipError_t value when a HIP call fails.
+ * not register; LA_ENOMEM when host memory or a host thread cannot be had;
+ * a positive hipError_t value when a HIP call fails.  No C++ exception
+ * leaves the library.
  * All device entry points are asynchronous on the stream passed in.
  */
 #ifndef SLIDEFORMER_AMD_LAYER_ADAM_H
@@ -26,6 +28,7 @@ extern "C" {
 #define LA_OK 0
 #define LA_EINVAL (-22)
 #define LA_EDTYPE (-95)
+#define LA_ENOMEM (-12)
 
 /* element types of p / g / m,v */
 #define LA_F32 0

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libs
 LA_OK = 0
 LA_EINVAL = -22
 LA_EDTYPE = -95
+LA_ENOMEM = -12
 
 LA_F32, LA_BF16, LA_F16 = 0, 1, 2
 

@@ -98,7 +98,7 @@ void worker_loop(la_disk* d)
 }
 
 int submit(la_disk* d, uint64_t key, void* buf, uint64_t bytes, bool write)
-{
+try {
     if (!d || (bytes > 0 && !buf)) return LA_EINVAL;
     std::lock_guard<std::mutex> lk(d->mu);
     auto it = d->fds.find(key);
@@ -125,6 +125,8 @@ int submit(la_disk* d, uint64_t key, void* buf, uint64_t bytes, bool write)
     }
     d->work_cv.notify_all();
     return LA_OK;
+} catch (...) {
+    return -ENOMEM;
 }
 
 }  // namespace

@@ -881,13 +881,14 @@ const char* la_strerror(int code)
     if (code == LA_OK) return "ok";
     if (code == LA_EINVAL) return "invalid argument (null/misaligned pointer, unknown id or bad size)";
     if (code == LA_EDTYPE) return "dtype triple not supported";
+    if (code == LA_ENOMEM) return "out of host memory or host threads";
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
     return "unknown error";
 }
 
 int la_create(int id, float lr, float beta1, float beta2, float eps, float weight_decay, int adamw_mode,
               int should_log)
-{
+try {
     HostState s;
     s.alpha = lr;
     s.betta1 = beta1;
@@ -905,6 +906,8 @@ int la_create(int id, float lr, float beta1, float beta2, float eps, float weigh
                     weight_decay, adamw_mode ? 1 : 0);
     }
     return LA_OK;
+} catch (...) {
+    return LA_ENOMEM;
 }
 
 int la_destroy(int id)
@@ -956,7 +959,7 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
 int la_adam_update_multi(int id, uint64_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
                          int bias_correction, int p_dtype, int g_dtype, int s_dtype, const la_segment_t* segs,
                          int count, const float* clip_coef, la_stream_t stream)
-{
+try {
     if (count < 0 || (count > 0 && !segs)) return LA_EINVAL;
     if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
     const bool registered = dt_valid(p_dtype) && dt_valid(g_dtype) && dt_valid(s_dtype) &&
@@ -1028,6 +1031,8 @@ int la_adam_update_multi(int id, uint64_t step, float lr, float beta1, float bet
         runs += seg_runs;
     }
     return flush();
+} catch (...) {
+    return LA_ENOMEM;
 }
 
 uint64_t la_grad_sqnorm_workspace(uint64_t n) { return norm_workspace_bytes(n); }

@@ -207,7 +207,7 @@ uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtyp
 }
 
 int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out)
-{
+try {
     if (!out) return LA_EINVAL;
     *out = nullptr;
     chunk_elems = chunk_elems / 16 * 16;
@@ -240,6 +240,8 @@ int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out)
     }
     *out = pl;
     return LA_OK;
+} catch (...) {
+    return LA_ENOMEM;
 }
 
 int la_pipeline_destroy(la_pipeline_t* pl)
@@ -259,9 +261,11 @@ int la_pipeline_destroy(la_pipeline_t* pl)
 }
 
 int la_pipeline_sync(la_pipeline_t* pl)
-{
+try {
     if (!pl) return LA_EINVAL;
     return settle_all(pl);
+} catch (...) {
+    return LA_ENOMEM;
 }
 
 int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads)
@@ -301,7 +305,7 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
                      int g_on_host, int s_dtype, void* m_host, void* v_host, uint64_t n, uint16_t* out,
                      int out_on_host, const float* clip_coef, void* workspace, uint64_t workspace_bytes,
                      la_stream_t after, int synchronize, la_pipeline_stats_t* stats)
-{
+try {
     const auto t0 = std::chrono::steady_clock::now();
     if (stats) std::memset(stats, 0, sizeof(*stats));
     if (!pl || !sc) return LA_EINVAL;
@@ -512,6 +516,10 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
                 std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count());
     }
     return LA_OK;
+} catch (...) {
+    // host allocation failed part-way: let the queued work land first
+    if (pl) (void)drain_streams(pl, LA_OK);
+    return LA_ENOMEM;
 }
 
 }  // extern "C"

@@ -32,6 +32,10 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
     assert L.la_abi_version() == version == 4
+    header = open(HEADER).read()
+    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM"):
+        value = int(re.search(rf"#define {name} \(?(-?\d+)\)?", header).group(1))
+        assert getattr(_lib, name) == value, name
 
 
 def test_library_is_gfx950_code_object():
@@ -110,6 +114,7 @@ def test_error_codes_without_launch():
     assert L.la_grad_norm_clip(1, None, 10, None, 0, None, 0, 1.0, None, None, None) == _lib.LA_EINVAL
     assert L.la_clip_coef(None, 1.0, None, None, None) == _lib.LA_EINVAL
     assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
+    assert b"memory" in L.la_strerror(_lib.LA_ENOMEM)
 
 
 def test_grad_sqnorm_workspace_is_bounded():
