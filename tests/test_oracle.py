@@ -130,6 +130,72 @@ def test_oracle_matches_compiled_reference(triple, mode):
     assert G.same_bits(_np_bits(v, sk), vb, sk).all()
 
 
+AVX2_WIDTH = [(("f32", "bf16", "f32"), 0), (("bf16", "bf16", "bf16"), 0), (("f32", "f32", "f32"), 8),
+              (("f16", "f16", "f16"), 8), (("f32", "f16", "f32"), 8)]
+
+
+@pytest.mark.parametrize("triple,width", AVX2_WIDTH, ids=lambda x: "-".join(x) if isinstance(x, tuple) else str(x))
+def test_oracle_body_width_matches_the_avx2_reference_build(triple, width):
+    """The reference's SIMD width follows the host ISA (builder.py:55-82,
+    simd.h:32-45,95-108): 16 lanes with AVX-512, 8 with AVX2 only.  Without
+    AVX-512, Step_AVX returns before its body for any triple with a bf16
+    operand (cpu_adam.h:117-122), so rounded_size stays 0 and every element
+    takes the scalar loop (cpu_adam_impl.cpp:29-34): the oracle's body_width=0.
+    The f32/f16 triples run the 8-lane body with an n mod 8 scalar tail.  The
+    AVX2 build compiled from the same sources (oracle/Makefile) must equal the
+    oracle at that width and differ from it at the others, on call sizes with
+    every tail length 0-15 and non-zero moments.  The product follows the
+    AVX-512 build (body_width=16)."""
+    if "avx2" not in O._cpu_flags() or "fma" not in O._cpu_flags():
+        pytest.skip("host cannot run the AVX2 build")
+    ref = O.load_ref("avx2")
+    if ref is None:
+        pytest.skip("oracle/_ref AVX2 build not present")
+    pk, gk, sk = triple
+    rng = np.random.default_rng(zlib.crc32(repr(triple).encode()))
+    sizes = tuple(64 + t for t in range(16)) + (4099,)
+    n = sum(sizes)
+    p0 = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(TD[pk])
+    m0 = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(TD[sk])
+    v0 = torch.from_numpy(np.abs(rng.normal(0, 1e-3, n)).astype(np.float32) ** 2).to(TD[sk])
+    grads = [torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(TD[gk]) for _ in range(2)]
+
+    p, m, v = p0.clone(), m0.clone(), v0.clone()
+    ref.create_adam(0, 1e-3, 0.9, 0.999, 1e-8, 0.05, True, False)
+    for st, g in enumerate(grads, start=1):
+        lo = 0
+        for size in sizes:
+            hi = lo + size
+            ref.adam_update(0, st, 1e-3, 0.9, 0.999, 1e-8, 0.05, True, p[lo:hi], g[lo:hi], m[lo:hi], v[lo:hi])
+            lo = hi
+    expect = (_np_bits(p, pk), _np_bits(m, sk), _np_bits(v, sk))
+
+    def oracle_at(bw):
+        pb, mb, vb = _np_bits(p0, pk), _np_bits(m0, sk), _np_bits(v0, sk)
+        opt = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.05, True)
+        for st, g in enumerate(grads, start=1):
+            gb = _np_bits(g, gk)
+            lo = 0
+            for size in sizes:
+                hi = lo + size
+                opt.update(st, 1e-3, 0.9, 0.999, 1e-8, 0.05, True, _view(pb, pk)[lo:hi], _view(gb, gk)[lo:hi],
+                           _view(mb, sk)[lo:hi], _view(vb, sk)[lo:hi], p16=KIND16[pk], g16=KIND16[gk],
+                           s16=KIND16[sk], body_width=bw)
+                lo = hi
+        return pb, mb, vb
+
+    def same(got):
+        return all(G.same_bits(e, o, k).all() for e, o, k in zip(expect, got, (pk, sk, sk)))
+
+    assert same(oracle_at(width))
+    # the inputs tell the widths apart: the scalar-only and 16-lane semantics
+    # give other bits than the 8-lane build and vice versa
+    others = [bw for bw in (0, 8, 16) if bw != width]
+    assert not same(oracle_at(others[0]))
+    if sk == "f32":
+        assert not same(oracle_at(others[1]))
+
+
 def test_oracle_clip_equals_reference_on_prescaled_grads():
     """clip_coef inside the oracle == the reference fed fl32(f32(g)*coef) through
     its (float, float, float) triple (cpu_adam_impl.cpp:187)."""
