@@ -137,7 +137,10 @@ def streamed(args):
     H2D/D2H GB/s, the isolated rates of each stage and the overlap (sum of
     isolated times / wall).  With --pageable the isolated copies are torch
     copy_ calls on the same pageable arrays, i.e. the HIP runtime's own
-    bounce-buffer path that the pipeline's staging replaces."""
+    bounce-buffer path that the pipeline's staging replaces.  --moments-in-hbm
+    keeps m and v in HBM (LayerAdam(moments_device=...)), so only the master
+    crosses the link; --host-grads puts the bf16 grads in page-locked host
+    memory, as the runtime's shared grad buffer is."""
     import ctypes
 
     import torch
@@ -166,20 +169,32 @@ def streamed(args):
     log(f"streamed {args.streamed}: n={n}, chunk={chunk}, slots={slots}")
     gen = torch.Generator(device=dev)
     gen.manual_seed(50)
-    host = []
-    for std in (0.02, 0.0, 0.0):
+    state = []
+    for idx, std in enumerate((0.02, 0.0, 0.0)):
+        if idx > 0 and args.moments_in_hbm:
+            state.append(torch.zeros(n, dtype=torch.float32, device=dev))
+            continue
         t = torch.empty(n, dtype=torch.float32, pin_memory=not args.pageable)
         piece = 256 * 1024 * 1024
         for lo in range(0, n, piece):
             hi = min(n, lo + piece)
             src = torch.randn(hi - lo, generator=gen, device=dev) * std if std else torch.zeros(hi - lo, device=dev)
             t[lo:hi].copy_(src)
-        host.append(t)
-    p, m, v = host
+        state.append(t)
+    p, m, v = state
+    host = [t for t in state if not t.is_cuda]
     g = (torch.randn(n, generator=gen, device=dev) * gstd).bfloat16()
+    if args.host_grads:
+        g = g.cpu().pin_memory()
     out = torch.empty(n, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
-    log(("pageable" if args.pageable else "pinned") + " state allocated and initialised")
+    log(("pageable" if args.pageable else "pinned") + " state allocated and initialised" +
+        (" (moments in HBM)" if args.moments_in_hbm else ""))
+    if args.moments_in_hbm:
+        workload = workload.replace("fp32 p/m/v in host RAM", "fp32 master in host RAM, fp32 moments in HBM")
+    if args.host_grads:
+        workload = workload.replace("bf16 grads and bf16 copy in HBM",
+                                    "bf16 grads in page-locked host RAM, bf16 copy in HBM")
 
     adam = LayerAdam(lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, overlap_host_chunks=args.overlap)
     adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads,
@@ -206,7 +221,8 @@ def streamed(args):
             walls.append(wall_ms)
             host_copy.append(copy_ms)
     wall = sum(walls) / len(walls)
-    h2d_bytes = d2h_bytes = 12 * n          # p, m, v each way; grads and the copy stay in HBM
+    d2h_bytes = 4 * len(host) * n                         # host-resident fp32 state, each way
+    h2d_bytes = d2h_bytes + (2 * n if args.host_grads else 0)
 
     # isolated stages: the same copies alone, and the update alone on resident buffers
     stream = torch.cuda.current_stream(dev)
@@ -223,25 +239,27 @@ def streamed(args):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
+    gbuf = torch.empty(chunk, dtype=torch.bfloat16, device=dev) if args.host_grads else None
+
     def h2d_only():
-        for arr in (p, m, v):
+        for arr in host + ([g] if args.host_grads else []):
             for lo in range(0, n, chunk):
                 hi = min(n, lo + chunk)
-                dbuf[:hi - lo].copy_(arr[lo:hi], non_blocking=True)
+                (gbuf if arr is g else dbuf)[:hi - lo].copy_(arr[lo:hi], non_blocking=True)
 
     def d2h_only():
-        for arr in (p, m, v):
+        for arr in host:
             for lo in range(0, n, chunk):
                 hi = min(n, lo + chunk)
                 arr[lo:hi].copy_(dbuf[:hi - lo], non_blocking=True)
 
     t_h2d = timed(h2d_only)
     t_d2h = timed(d2h_only)
-    del dbuf
-    pd, md, vd = (x.to(dev) for x in (p, m, v))
-    t_comp = timed(lambda: adam.step_chunk(pd, g, md, vd, dict(adam.defaults, step=args.warmup + args.steps + 1),
+    del dbuf, gbuf
+    pd, md, vd, gd = (x.to(dev) for x in (p, m, v, g))
+    t_comp = timed(lambda: adam.step_chunk(pd, gd, md, vd, dict(adam.defaults, step=args.warmup + args.steps + 1),
                                            bf16_out=out))
-    del pd, md, vd
+    del pd, md, vd, gd
     res = {
         "metric": "streamed LayerAdam step (host-resident fp32 state), Gparams/s",
         "value": round(n / (wall * 1e-3) / 1e9, 3),
@@ -256,6 +274,8 @@ def streamed(args):
         "config": {"workload": workload, "params": n, "chunk_elems": chunk, "slots": slots,
                    "elements_per_call": call, "overlap_host_chunks": bool(args.overlap),
                    "host_memory": "pageable" if args.pageable else "pinned",
+                   "moments": "HBM" if args.moments_in_hbm else "host",
+                   "grads": "page-locked host" if args.host_grads else "HBM",
                    "pageable_copies": ("none" if not args.pageable else
                                        "HIP runtime bounce buffers" if args.no_staging else
                                        f"page-locked slot twins, host threads {args.host_threads or 'default'}")},
@@ -289,7 +309,9 @@ def streamed_model(args):
     a global grad norm accumulated in sliding order, one clip coefficient, then
     each layer streamed through HBM in 64 MB chunks (16 Mi fp32 elements, 3
     slots), in sliding order (lm_head, L31 ... L0, embed;
-    offload_transformer.py:265-301)."""
+    offload_transformer.py:265-301).  --moments-in-hbm keeps every layer's m
+    and v in HBM (64 GB; LayerAdam(moments_device=...)), so only the master
+    crosses the link."""
     import torch
 
     from slideformer_amd import LayerAdam
@@ -303,7 +325,8 @@ def streamed_model(args):
     log(f"streamed c3 model: {len(sizes)} layers, {n_total} params, chunk={chunk}, slots={slots}")
     gen = torch.Generator(device=dev)
     gen.manual_seed(70)
-    adam = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    adam = LayerAdam(lr=1e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01,
+                     moments_device=dev if args.moments_in_hbm else None)
     adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads)
     params, grads, outs = [], [], []
     piece = 256 * 1024 * 1024
@@ -352,7 +375,16 @@ def streamed_model(args):
         span_sum = [a + b for a, b in zip(span_sum, spans)]
         log(f"step {i + 1}: {w:.3f} s")
     wall = sum(walls) / len(walls)
-    each_way = 12 * n_total
+    each_way = (4 if args.moments_in_hbm else 12) * n_total
+    workload = ("C3: Llama-3.1-8B-shaped model, embed + 32 decoder layers + norm/lm_head "
+                "(8,030,261,248 params); fp32 p/m/v in pageable host RAM (the reference's "
+                "allocation), staged through page-locked slot twins by native host threads, "
+                "streamed in 64 MB chunks x 3 slots in sliding order; global clip 1.0; bf16 "
+                "grads and copies in HBM")
+    if args.moments_in_hbm:
+        workload = workload.replace("fp32 p/m/v in pageable host RAM (the reference's allocation)",
+                                    "fp32 master in pageable host RAM (the reference's allocation), "
+                                    "fp32 moments in HBM")
     res = {
         "metric": "streamed LayerAdam full-model step (host-resident fp32 state), Gparams/s",
         "value": round(n_total / wall / 1e9, 3),
@@ -364,11 +396,7 @@ def streamed_model(args):
         "higher_is_better": True,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": ("C3: Llama-3.1-8B-shaped model, embed + 32 decoder layers + norm/lm_head "
-                                "(8,030,261,248 params); fp32 p/m/v in pageable host RAM (the reference's "
-                                "allocation), staged through page-locked slot twins by native host threads, "
-                                "streamed in 64 MB chunks x 3 slots in sliding order; global clip 1.0; bf16 "
-                                "grads and copies in HBM"),
+        "config": {"workload": workload, "moments": "HBM" if args.moments_in_hbm else "host",
                    "params": n_total, "layers": len(sizes), "chunk_elems": chunk, "slots": slots},
         "h2d_gbs_effective": round(each_way / wall / 1e9, 2),
         "d2h_gbs_effective": round(each_way / wall / 1e9, 2),
@@ -628,6 +656,10 @@ def main():
                     help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
     ap.add_argument("--slots", type=int, default=0,
                     help="with --streamed c3-layer|c5: pipeline slots (default: the config's)")
+    ap.add_argument("--moments-in-hbm", action="store_true",
+                    help="--streamed: m and v stay in HBM, only the fp32 master is streamed")
+    ap.add_argument("--host-grads", action="store_true",
+                    help="--streamed: bf16 grads in page-locked host memory (the runtime's grad buffer)")
     ap.add_argument("--no-staging", action="store_true",
                     help="with --streamed --pageable: leave pageable arrays to the HIP runtime's bounce buffers")
     ap.add_argument("--streamed", choices=["c5", "c3", "c3-layer"], default=None,

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 4
+#define LA_ABI_VERSION 5
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -166,36 +166,43 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  * Replaces the runtime's chunk pipeline around the update: CPU fp32->bf16
  * cast + H2D (transformer_layer.py:297-305), grad D2H in chunks with
  * per-chunk events (:343-422) and the update thread consuming them (:453-493).
- * Here p, m, v are copied in, updated on the GPU and copied back, chunk by
- * chunk, on three HIP streams (H2D, compute, D2H) so that transfers in both
- * directions overlap the update of other chunks.
+ * Here the host-resident arrays are copied in, updated on the GPU and copied
+ * back, chunk by chunk, on three HIP streams (H2D, compute, D2H) so that
+ * transfers in both directions overlap the update of other chunks.
+ *
+ * Placement: `on_host` has one bit per array.  A set bit means the array is
+ * in host memory and streams through the device slots; a clear bit means it
+ * is in device memory and the update reads and writes it in place.  The
+ * reference runtime keeps everything on the host (LA_ON_HOST_P|M|V|G, plus
+ * OUT when the bf16 copy goes to host staging); keeping the moments in HBM
+ * (LA_ON_HOST_P | LA_ON_HOST_G) moves 6 B/param in and 4 B/param out instead
+ * of 14 and 12.
  *
  * la_pipeline_create: chunk_elems is rounded down to a multiple of 16 (only
  *   the last chunk of a call then holds the reference's scalar tail); 1..16
  *   staging slots.  Creates the streams and events; allocates no memory.
  * la_pipeline_workspace_bytes: device staging bytes the caller must provide
- *   (256-byte aligned) for the given element types and placements.
- * la_pipeline_step: one reference adam_update over n elements whose p, m, v
- *   live in host memory (pinned for full speed).  g is on the host when
- *   g_on_host, else on the device; the bf16 copy `out` (nullable) goes to the
- *   host when out_on_host, else stays on the device.  Work queued on `after`
- *   before the call runs first; work queued on `after` later sees the
- *   result.  synchronize != 0 (or stats != NULL) waits for completion of
- *   this call and of every earlier one.  With synchronize == 0 the call
- *   returns once its work is queued, and work queued on `after` later is not
- *   ordered after it; its host arrays, device outputs, workspace and staging
- *   must then stay valid, and must not be read or written by the caller,
- *   until a synchronizing call or la_pipeline_sync.  The slot ring carries
- *   over from call to call, so consecutive calls on disjoint host ranges
- *   (the runtime's one call per chunk) keep both copy directions busy; a call
- *   touching host bytes of an earlier unsettled call, or using another
- *   workspace or slot layout (element types, g/out placement) than the
- *   previous call, settles everything first.
+ *   (256-byte aligned) for the given element types and placement.
+ * la_pipeline_step: one reference adam_update over n elements (p, m, v, g
+ *   and the nullable bf16 copy `out` placed as `on_host` says; host arrays
+ *   page-locked for full speed).  Work queued on `after` before the call
+ *   runs first; work queued on `after` later sees the result.
+ *   synchronize != 0 (or stats != NULL) waits for completion of this call
+ *   and of every earlier one.  With synchronize == 0 the call returns once
+ *   its work is queued, and work queued on `after` later is not ordered
+ *   after it; its arrays, workspace and staging must then stay valid, and
+ *   must not be read or written by the caller, until a synchronizing call or
+ *   la_pipeline_sync.  The slot ring carries over from call to call, so
+ *   consecutive calls on disjoint host ranges (the runtime's one call per
+ *   chunk) keep both copy directions busy; a call touching host bytes of an
+ *   earlier unsettled call, or using another workspace or slot layout
+ *   (element types, placement) than the previous call, settles everything
+ *   first.  Device-resident arrays are updated in call order on one stream.
  *   One pipeline object must not be used by two threads at once.
  * la_pipeline_sync: wait until every queued call is complete in host memory.
  * la_pipeline_set_host_staging: attach caller-owned page-locked host memory
  *   (256-byte aligned, at least la_pipeline_workspace_bytes() for the call's
- *   types and placements) and the number of host copy threads (0 = up to 16),
+ *   types and placement) and the number of host copy threads (0 = up to 16),
  *   or detach it with pinned = NULL.  While attached, la_pipeline_step copies
  *   every pageable host array through it: `threads` host threads copy each
  *   chunk into the page-locked twin of its slot and the results back out, and
@@ -204,6 +211,13 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   attachment settles every queued call first.  No
  *   reference counterpart: the reference updates pageable state on the CPU.
  */
+#define LA_ON_HOST_P 1u
+#define LA_ON_HOST_M 2u
+#define LA_ON_HOST_V 4u
+#define LA_ON_HOST_G 8u
+#define LA_ON_HOST_OUT 16u
+#define LA_ON_HOST_ALL 31u
+
 typedef struct la_pipeline la_pipeline_t;
 
 typedef struct {
@@ -219,16 +233,16 @@ typedef struct {
 } la_pipeline_stats_t;
 
 uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtype, int g_dtype,
-                                     int s_dtype, int g_on_host, int out_on_host);
+                                     int s_dtype, unsigned on_host);
 int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out);
 int la_pipeline_destroy(la_pipeline_t* pl);
 int la_pipeline_sync(la_pipeline_t* pl);
 int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes, int threads);
-int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host,
-                     int g_dtype, const void* g, int g_on_host, int s_dtype, void* m_host,
-                     void* v_host, uint64_t n, uint16_t* out, int out_on_host,
-                     const float* clip_coef, void* workspace, uint64_t workspace_bytes,
-                     la_stream_t after, int synchronize, la_pipeline_stats_t* stats);
+int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p, int g_dtype,
+                     const void* g, int s_dtype, void* m, void* v, uint64_t n, uint16_t* out,
+                     unsigned on_host, const float* clip_coef, void* workspace,
+                     uint64_t workspace_bytes, la_stream_t after, int synchronize,
+                     la_pipeline_stats_t* stats);
 
 /*
  * Asynchronous file offload of host state buffers (the NVMe moment offload).

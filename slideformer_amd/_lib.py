@@ -24,6 +24,10 @@ LA_ENOMEM = -12
 
 LA_F32, LA_BF16, LA_F16 = 0, 1, 2
 
+# la_pipeline_step placement bits: a set bit = that array is in host memory
+LA_ON_HOST_P, LA_ON_HOST_M, LA_ON_HOST_V, LA_ON_HOST_G, LA_ON_HOST_OUT = 1, 2, 4, 8, 16
+LA_ON_HOST_ALL = 31
+
 # every exported symbol of include/layer_adam.h
 EXPORTED = (
     "la_abi_version",
@@ -135,7 +139,7 @@ def _declare(L):
     L.la_grad_norm_clip.restype = i
     L.la_clip_coef.argtypes = [P, f, P, P, P]
     L.la_clip_coef.restype = i
-    L.la_pipeline_workspace_bytes.argtypes = [u64, i, i, i, i, i, i]
+    L.la_pipeline_workspace_bytes.argtypes = [u64, i, i, i, i, ctypes.c_uint]
     L.la_pipeline_workspace_bytes.restype = u64
     L.la_pipeline_create.argtypes = [u64, i, ctypes.POINTER(P)]
     L.la_pipeline_create.restype = i
@@ -145,7 +149,7 @@ def _declare(L):
     L.la_pipeline_sync.restype = i
     L.la_pipeline_set_host_staging.argtypes = [P, P, u64, i]
     L.la_pipeline_set_host_staging.restype = i
-    L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, i, P, P, u64, P, i, P, P, u64, P, i,
+    L.la_pipeline_step.argtypes = [P, SP, i, P, i, P, i, P, P, u64, P, ctypes.c_uint, P, P, u64, P, i,
                                    ctypes.POINTER(LaPipelineStats)]
     L.la_pipeline_step.restype = i
     L.la_disk_create.argtypes = [ctypes.c_char_p, i, ctypes.POINTER(P)]

@@ -4,10 +4,13 @@
 // fp32 master and moments on the CPU, transformer_layer.py:192-196 and
 // layer_adam.py:161-173), one call streams the state through HBM in chunks:
 //
-//   h2d stream :  copy p, m, v (and g when it is on the host) of chunk i into slot i % S
-//   compute    :  wait for that copy, run the fused update on the slot
-//   d2h stream :  wait for the update, copy p, m, v (and the bf16 copy when it goes
-//                 to the host) back, then free the slot for chunk i + S
+//   h2d stream :  copy the host-resident arrays among p, m, v, g of chunk i into
+//                 slot i % S
+//   compute    :  wait for that copy, run the fused update on the slot (arrays
+//                 that live in device memory are read and written in place)
+//   d2h stream :  wait for the update, copy the host-resident p, m, v (and the
+//                 bf16 copy when it goes to the host) back, then free the slot
+//                 for chunk i + S
 //
 // The reference does the same split with threads and a queue of per-chunk
 // events (transformer_layer.py:297-305 H2D, :343-422 D2H, :453-493 update);
@@ -87,23 +90,26 @@ struct SlotLayout {
     uint64_t p, m, v, g, out, slot_bytes;
 };
 
-SlotLayout slot_layout(uint64_t chunk, int p_dt, int g_dt, int s_dt, int g_on_host, int out_on_host)
+// A slot holds one chunk of every host-resident array (on_host bits).
+SlotLayout slot_layout(uint64_t chunk, int p_dt, int g_dt, int s_dt, unsigned on_host)
 {
     SlotLayout L{};
     uint64_t off = 0;
     L.p = off;
-    off += round_up(chunk * esize(p_dt), kAlign);
+    if (on_host & LA_ON_HOST_P) off += round_up(chunk * esize(p_dt), kAlign);
     L.m = off;
-    off += round_up(chunk * esize(s_dt), kAlign);
+    if (on_host & LA_ON_HOST_M) off += round_up(chunk * esize(s_dt), kAlign);
     L.v = off;
-    off += round_up(chunk * esize(s_dt), kAlign);
+    if (on_host & LA_ON_HOST_V) off += round_up(chunk * esize(s_dt), kAlign);
     L.g = off;
-    if (g_on_host) off += round_up(chunk * esize(g_dt), kAlign);
+    if (on_host & LA_ON_HOST_G) off += round_up(chunk * esize(g_dt), kAlign);
     L.out = off;
-    if (out_on_host) off += round_up(chunk * 2, kAlign);
+    if (on_host & LA_ON_HOST_OUT) off += round_up(chunk * 2, kAlign);
     L.slot_bytes = off;
     return L;
 }
+
+bool misaligned(const void* ptr, int bytes) { return reinterpret_cast<uintptr_t>(ptr) % static_cast<uintptr_t>(bytes); }
 
 int rc_of(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
 
@@ -198,12 +204,11 @@ void destroy_events(la_pipeline* pl)
 extern "C" {
 
 uint64_t la_pipeline_workspace_bytes(uint64_t chunk_elems, int slots, int p_dtype, int g_dtype, int s_dtype,
-                                     int g_on_host, int out_on_host)
+                                     unsigned on_host)
 {
     chunk_elems = chunk_elems / 16 * 16;
-    if (chunk_elems == 0 || slots <= 0) return 0;
-    return slot_layout(chunk_elems, p_dtype, g_dtype, s_dtype, g_on_host, out_on_host).slot_bytes *
-           static_cast<uint64_t>(slots);
+    if (chunk_elems == 0 || slots <= 0 || (on_host & ~LA_ON_HOST_ALL)) return 0;
+    return slot_layout(chunk_elems, p_dtype, g_dtype, s_dtype, on_host).slot_bytes * static_cast<uint64_t>(slots);
 }
 
 int la_pipeline_create(uint64_t chunk_elems, int slots, la_pipeline_t** out)
@@ -301,10 +306,10 @@ int la_pipeline_set_host_staging(la_pipeline_t* pl, void* pinned, uint64_t bytes
     return LA_OK;
 }
 
-int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p_host, int g_dtype, const void* g,
-                     int g_on_host, int s_dtype, void* m_host, void* v_host, uint64_t n, uint16_t* out,
-                     int out_on_host, const float* clip_coef, void* workspace, uint64_t workspace_bytes,
-                     la_stream_t after, int synchronize, la_pipeline_stats_t* stats)
+int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, void* p, int g_dtype, const void* g,
+                     int s_dtype, void* m, void* v, uint64_t n, uint16_t* out, unsigned on_host,
+                     const float* clip_coef, void* workspace, uint64_t workspace_bytes, la_stream_t after,
+                     int synchronize, la_pipeline_stats_t* stats)
 try {
     const auto t0 = std::chrono::steady_clock::now();
     if (stats) std::memset(stats, 0, sizeof(*stats));
@@ -319,34 +324,39 @@ try {
                                      nullptr, nullptr);
         if (rc != LA_OK) return rc;
     }
+    if (on_host & ~LA_ON_HOST_ALL) return LA_EINVAL;
     if (n == 0) return LA_OK;
-    if (!p_host || !g || !m_host || !v_host || !workspace) return LA_EINVAL;
-    if (!g_on_host && reinterpret_cast<uintptr_t>(g) % static_cast<uintptr_t>(esize(g_dtype))) return LA_EINVAL;
-    if (out && !out_on_host && (reinterpret_cast<uintptr_t>(out) & 1u)) return LA_EINVAL;
-    if (clip_coef && (reinterpret_cast<uintptr_t>(clip_coef) & 3u)) return LA_EINVAL;
-    if (out_on_host && !out) return LA_EINVAL;
-    if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return LA_EINVAL;
-    const SlotLayout L = slot_layout(pl->chunk, p_dtype, g_dtype, s_dtype, g_on_host, out_on_host && out);
+    if (!p || !g || !m || !v || !workspace) return LA_EINVAL;
+    const bool hp = on_host & LA_ON_HOST_P, hm = on_host & LA_ON_HOST_M, hv = on_host & LA_ON_HOST_V;
+    const bool hg = on_host & LA_ON_HOST_G, ho = on_host & LA_ON_HOST_OUT;
+    if (ho && !out) return LA_EINVAL;
+    const int pb = esize(p_dtype), gb = esize(g_dtype), sb = esize(s_dtype);
+    // device-resident arrays are used in place: whole elements only
+    if ((!hp && misaligned(p, pb)) || (!hm && misaligned(m, sb)) || (!hv && misaligned(v, sb)) ||
+        (!hg && misaligned(g, gb)) || (out && !ho && misaligned(out, 2)))
+        return LA_EINVAL;
+    if (clip_coef && misaligned(clip_coef, 4)) return LA_EINVAL;
+    if (misaligned(workspace, static_cast<int>(kAlign))) return LA_EINVAL;
+    const SlotLayout L = slot_layout(pl->chunk, p_dtype, g_dtype, s_dtype, on_host);
     const uint64_t ws_need = L.slot_bytes * static_cast<uint64_t>(pl->slots);
     if (workspace_bytes < ws_need) return LA_EINVAL;
 
     // which host arrays go through the page-locked staging (pageable ones, when it is attached)
     bool st_p = false, st_m = false, st_v = false, st_g = false, st_o = false;
     if (pl->host_staging) {
-        st_p = !page_locked(p_host);
-        st_m = !page_locked(m_host);
-        st_v = !page_locked(v_host);
-        st_g = g_on_host && !page_locked(g);
-        st_o = out && out_on_host && !page_locked(out);
+        st_p = hp && !page_locked(p);
+        st_m = hm && !page_locked(m);
+        st_v = hv && !page_locked(v);
+        st_g = hg && !page_locked(g);
+        st_o = ho && !page_locked(out);
     }
     const bool staged = st_p || st_m || st_v || st_g || st_o;
     if (staged && pl->host_staging_bytes < ws_need) return LA_EINVAL;
 
-    const int pb = esize(p_dtype), gb = esize(g_dtype), sb = esize(s_dtype);
     char* ws = static_cast<char*>(workspace);
-    char* ph = static_cast<char*>(p_host);
-    char* mh = static_cast<char*>(m_host);
-    char* vh = static_cast<char*>(v_host);
+    char* pp = static_cast<char*>(p);
+    char* mp = static_cast<char*>(m);
+    char* vp = static_cast<char*>(v);
     const char* gp = static_cast<const char*>(g);
     char* op = reinterpret_cast<char*>(out);
     const uint64_t nchunks = (n + pl->chunk - 1) / pl->chunk;
@@ -361,15 +371,16 @@ try {
     // everything first; otherwise this call streams on behind the earlier ones.
     std::pair<uintptr_t, uintptr_t> ranges[5];
     int nranges = 0;
-    auto add_range = [&](const void* ptr, uint64_t bytes) {
+    auto add_range = [&](bool host, const void* ptr, uint64_t bytes) {
+        if (!host) return;
         const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr);
         ranges[nranges++] = {lo, lo + bytes};
     };
-    add_range(ph, n * pb);
-    add_range(mh, n * sb);
-    add_range(vh, n * sb);
-    if (g_on_host) add_range(gp, n * gb);
-    if (out && out_on_host) add_range(op, n * 2);
+    add_range(hp, pp, n * pb);
+    add_range(hm, mp, n * sb);
+    add_range(hv, vp, n * sb);
+    add_range(hg, gp, n * gb);
+    add_range(ho, op, n * 2);
     bool clash = pl->touched.size() > 4096;
     // another workspace or slot layout than the previous call's: the slots of
     // the two layouts overlap, so earlier work must be finished first
@@ -428,57 +439,54 @@ try {
             if (rc != LA_OK) return drain_streams(pl, rc);
         }
         if (staged) {
-            if (st_p) add_pieces(pieces, hs + L.p, ph + off * pb, k * pb);
-            if (st_m) add_pieces(pieces, hs + L.m, mh + off * sb, k * sb);
-            if (st_v) add_pieces(pieces, hs + L.v, vh + off * sb, k * sb);
+            if (st_p) add_pieces(pieces, hs + L.p, pp + off * pb, k * pb);
+            if (st_m) add_pieces(pieces, hs + L.m, mp + off * sb, k * sb);
+            if (st_v) add_pieces(pieces, hs + L.v, vp + off * sb, k * sb);
             if (st_g) add_pieces(pieces, hs + L.g, gp + off * gb, k * gb);
             host_copy();
         }
+        // the addresses the update uses: a slot region for host arrays, the array itself otherwise
+        char* pd = hp ? slot + L.p : pp + off * pb;
+        char* md = hm ? slot + L.m : mp + off * sb;
+        char* vd = hv ? slot + L.v : vp + off * sb;
+        const void* gd = hg ? static_cast<const void*>(slot + L.g) : static_cast<const void*>(gp + off * gb);
+        uint16_t* od = nullptr;
+        if (out) od = ho ? reinterpret_cast<uint16_t*>(slot + L.out) : out + off;
+
         if (pl->slot_used[s]) LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->ev_d2h[s], 0));
-        LA_STEP_TRY(hipMemcpyAsync(slot + L.p, st_p ? hs + L.p : ph + off * pb, k * pb, hipMemcpyHostToDevice,
-                                   pl->h2d));
-        LA_STEP_TRY(hipMemcpyAsync(slot + L.m, st_m ? hs + L.m : mh + off * sb, k * sb, hipMemcpyHostToDevice,
-                                   pl->h2d));
-        LA_STEP_TRY(hipMemcpyAsync(slot + L.v, st_v ? hs + L.v : vh + off * sb, k * sb, hipMemcpyHostToDevice,
-                                   pl->h2d));
-        h2d_bytes += k * (pb + 2 * sb);
-        const void* gdev = gp + off * gb;
-        if (g_on_host) {
-            LA_STEP_TRY(hipMemcpyAsync(slot + L.g, st_g ? hs + L.g : gp + off * gb, k * gb, hipMemcpyHostToDevice,
-                                       pl->h2d));
-            h2d_bytes += k * gb;
-            gdev = slot + L.g;
-        }
+        auto copy_in = [&](bool host, bool st, char* dst, uint64_t region, const char* src, uint64_t bytes) {
+            if (!host) return hipSuccess;
+            h2d_bytes += bytes;
+            return hipMemcpyAsync(dst, st ? hs + region : src, bytes, hipMemcpyHostToDevice, pl->h2d);
+        };
+        LA_STEP_TRY(copy_in(hp, st_p, pd, L.p, pp + off * pb, k * pb));
+        LA_STEP_TRY(copy_in(hm, st_m, md, L.m, mp + off * sb, k * sb));
+        LA_STEP_TRY(copy_in(hv, st_v, vd, L.v, vp + off * sb, k * sb));
+        LA_STEP_TRY(copy_in(hg, st_g, slot + L.g, L.g, gp + off * gb, k * gb));
         LA_STEP_TRY(hipEventRecord(pl->ev_h2d[s], pl->h2d));
 
         LA_STEP_TRY(hipStreamWaitEvent(pl->comp, pl->ev_h2d[s], 0));
-        uint16_t* odev = nullptr;
-        if (out) odev = out_on_host ? reinterpret_cast<uint16_t*>(slot + L.out) : out + off;
-        const int rc = la_adamw_step(sc, p_dtype, slot + L.p, g_dtype, gdev, s_dtype, slot + L.m, slot + L.v, k,
-                                     odev, clip_coef, pl->comp);
+        const int rc = la_adamw_step(sc, p_dtype, pd, g_dtype, gd, s_dtype, md, vd, k, od, clip_coef, pl->comp);
         if (rc != LA_OK) return drain_streams(pl, rc);
         LA_STEP_TRY(hipEventRecord(pl->ev_comp[s], pl->comp));
 
         LA_STEP_TRY(hipStreamWaitEvent(pl->d2h, pl->ev_comp[s], 0));
-        LA_STEP_TRY(hipMemcpyAsync(st_p ? hs + L.p : ph + off * pb, slot + L.p, k * pb, hipMemcpyDeviceToHost,
-                                   pl->d2h));
-        LA_STEP_TRY(hipMemcpyAsync(st_m ? hs + L.m : mh + off * sb, slot + L.m, k * sb, hipMemcpyDeviceToHost,
-                                   pl->d2h));
-        LA_STEP_TRY(hipMemcpyAsync(st_v ? hs + L.v : vh + off * sb, slot + L.v, k * sb, hipMemcpyDeviceToHost,
-                                   pl->d2h));
-        d2h_bytes += k * (pb + 2 * sb);
-        if (out && out_on_host) {
-            LA_STEP_TRY(hipMemcpyAsync(st_o ? hs + L.out : op + off * 2, slot + L.out, k * 2, hipMemcpyDeviceToHost,
-                                       pl->d2h));
-            d2h_bytes += k * 2;
-        }
+        auto copy_out = [&](bool host, bool st, char* dst, uint64_t region, const char* src, uint64_t bytes) {
+            if (!host) return hipSuccess;
+            d2h_bytes += bytes;
+            return hipMemcpyAsync(st ? hs + region : dst, src, bytes, hipMemcpyDeviceToHost, pl->d2h);
+        };
+        LA_STEP_TRY(copy_out(hp, st_p, pp + off * pb, L.p, pd, k * pb));
+        LA_STEP_TRY(copy_out(hm, st_m, mp + off * sb, L.m, md, k * sb));
+        LA_STEP_TRY(copy_out(hv, st_v, vp + off * sb, L.v, vd, k * sb));
+        LA_STEP_TRY(copy_out(ho, st_o, op + off * 2, L.out, reinterpret_cast<const char*>(od), k * 2));
         LA_STEP_TRY(hipEventRecord(pl->ev_d2h[s], pl->d2h));
         pl->slot_used[s] = 1;
         pl->issued++;
         // the results of staged arrays are owed until they leave the twin
-        if (st_p) add_pieces(pl->owed[s], ph + off * pb, hs + L.p, k * pb);
-        if (st_m) add_pieces(pl->owed[s], mh + off * sb, hs + L.m, k * sb);
-        if (st_v) add_pieces(pl->owed[s], vh + off * sb, hs + L.v, k * sb);
+        if (st_p) add_pieces(pl->owed[s], pp + off * pb, hs + L.p, k * pb);
+        if (st_m) add_pieces(pl->owed[s], mp + off * sb, hs + L.m, k * sb);
+        if (st_v) add_pieces(pl->owed[s], vp + off * sb, hs + L.v, k * sb);
         if (st_o) add_pieces(pl->owed[s], op + off * 2, hs + L.out, k * 2);
     }
     LA_STEP_TRY(hipEventRecord(pl->t_h2d_end, pl->h2d));

@@ -13,10 +13,11 @@ Device tensors are updated in place, asynchronously on the current HIP stream.
 Host tensors (the reference's layout: fp32 master and moments in CPU RAM) are
 streamed through HBM in 16 Mi-element chunks by the library's native
 three-stream pipeline (H2D / update / D2H overlapped) and the call returns
-after completion, as the reference's CPU call does; grads and the bf16 copy may
-then live on the host or on the device.  Pageable host arrays are copied
-through page-locked staging by native host threads.  There is no CPU
-arithmetic path.
+after completion, as the reference's CPU call does.  Each array of a call may
+be on the host or on the one device; only the host-resident ones cross the
+host link (``LayerAdam(moments_device=...)`` keeps the moments in HBM beside a
+host-resident master).  Pageable host arrays are copied through page-locked
+staging by native host threads.  There is no CPU arithmetic path.
 
 Additions, all keyword-only so that positional signatures are unchanged:
 ``bf16_out=`` (the bf16 compute copy written in the same pass), ``clip_coef=``
@@ -96,8 +97,9 @@ class HostStreamer:
     def _bytes(self, key) -> int:
         return self.lib.la_pipeline_workspace_bytes(self.chunk, self.slots, *[int(k) for k in key])
 
-    def workspace(self, pc, gc, sc, g_on_host, out_on_host) -> torch.Tensor:
-        key = (pc, gc, sc, g_on_host, out_on_host)
+    def workspace(self, pc, gc, sc, on_host) -> torch.Tensor:
+        """Device staging for one element-type triple and placement (la_pipeline_workspace_bytes)."""
+        key = (pc, gc, sc, on_host)
         ws = self._ws.get(key)
         if ws is None:
             ws = torch.empty(self._bytes(key) + 256, dtype=torch.uint8, device=self.device)
@@ -119,23 +121,22 @@ class HostStreamer:
                                                          self.host_threads),
                    "la_pipeline_set_host_staging")
 
-    def step(self, scalars, pc, params, gc, grads, g_on_host, sc, exp_avg, exp_avg_sq, n, bf16_out,
-             out_on_host, clip_coef, stream_handle, synchronize: bool = True):
-        """One la_pipeline_step.  With synchronize=False it returns once the work
-        is queued (statistics then None); ``sync()`` completes it."""
-        key = (pc, gc, sc, g_on_host, out_on_host)
+    def step(self, scalars, pc, params, gc, grads, sc, exp_avg, exp_avg_sq, n, bf16_out, on_host,
+             clip_coef, stream_handle, synchronize: bool = True):
+        """One la_pipeline_step; ``on_host`` is its placement mask (``_placement``).
+        With synchronize=False it returns once the work is queued (statistics
+        then None); ``sync()`` completes it."""
+        key = (pc, gc, sc, on_host)
         ws = self.workspace(*key)
-        host = [params, exp_avg, exp_avg_sq] + ([grads] if g_on_host else []) + \
-            ([bf16_out] if out_on_host else [])
+        host = [t for t in (params, grads, exp_avg, exp_avg_sq, bf16_out) if t is not None and not t.is_cuda]
         self._attach_host_staging(key, self.stage_pageable and not all(t.is_pinned() for t in host))
         base = ws.data_ptr()
         aligned = (base + 255) // 256 * 256
         stats = _lib.LaPipelineStats() if synchronize else None
         rc = self.lib.la_pipeline_step(
-            self.handle, ctypes.byref(scalars), pc, params.data_ptr(), gc, grads.data_ptr(),
-            int(g_on_host), sc, exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n,
-            None if bf16_out is None else bf16_out.data_ptr(), int(out_on_host),
-            None if clip_coef is None else clip_coef.data_ptr(), aligned,
+            self.handle, ctypes.byref(scalars), pc, params.data_ptr(), gc, grads.data_ptr(), sc,
+            exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n, None if bf16_out is None else bf16_out.data_ptr(),
+            on_host, None if clip_coef is None else clip_coef.data_ptr(), aligned,
             ws.numel() - (aligned - base), stream_handle, int(synchronize),
             None if stats is None else ctypes.byref(stats))
         _lib.check(rc, "la_pipeline_step")
@@ -166,6 +167,16 @@ def _stream_handle(stream, device) -> int:
     if stream is None:
         stream = torch.cuda.current_stream(device)
     return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _placement(params, grads, exp_avg, exp_avg_sq, bf16_out) -> int:
+    """la_pipeline_step's ``on_host`` mask: one bit per array in host memory."""
+    mask = 0
+    for t, bit in ((params, _lib.LA_ON_HOST_P), (exp_avg, _lib.LA_ON_HOST_M), (exp_avg_sq, _lib.LA_ON_HOST_V),
+                   (grads, _lib.LA_ON_HOST_G), (bf16_out, _lib.LA_ON_HOST_OUT)):
+        if t is not None and not t.is_cuda:
+            mask |= bit
+    return mask
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -244,9 +255,15 @@ class LayerAdam:
             device: Optional[torch.device] = None,
             pin_host_state: bool = False,
             overlap_host_chunks: bool = False,
+            moments_device: Optional[torch.device] = None,
     ):
         """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
         ``device``: the HIP device that updates host-resident state (default: current);
+        ``moments_device``: a HIP device on which ``add_layer_params`` allocates
+        ``exp_avg`` / ``exp_avg_sq`` (default: beside the params, as the
+        reference does).  With a host-resident master (the runtime's layout) the
+        moments then stay in HBM and each step moves 6 B/param to the device
+        and 4 B/param back instead of 14 and 12;
         ``pin_host_state``: allocate host-resident moments in page-locked memory
         (streamed without staging copies; the reference allocates pageable memory,
         which the pipeline stages through page-locked buffers);
@@ -280,6 +297,12 @@ class LayerAdam:
         self.device = torch.device(device) if device is not None else None
         self.pin_host_state = pin_host_state
         self.overlap_host_chunks = overlap_host_chunks
+        self.moments_device = torch.device(moments_device) if moments_device is not None else None
+        if self.moments_device is not None and self.moments_device.type != 'cuda':
+            raise ValueError(f"moments_device must be a HIP device, got {self.moments_device}")
+        if self.moments_device is not None and nvme_offload_fraction > 0.0:
+            raise ValueError("moments_device and nvme_offload_fraction > 0 exclude each other: "
+                             "the file offload moves host-resident moments")
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
         assert 0.0 <= nvme_offload_fraction <= 1.0
@@ -338,7 +361,7 @@ class LayerAdam:
         params = list(params)
         if not params:
             return -1
-        device = params[0].device
+        device = self.moments_device or params[0].device
         if self.offloader is not None and device.type != 'cpu':
             # as in the reference, the file offload moves host-resident moments
             raise RuntimeError("nvme_offload_fraction > 0 needs host-resident params and state")
@@ -455,28 +478,21 @@ class LayerAdam:
             if clip_coef.dtype != torch.float32 or clip_coef.numel() < 1 or clip_coef.device.type != 'cuda':
                 raise RuntimeError("clip_coef must be a float32 device tensor")
 
-        state_devs = {t.device for t in (params, exp_avg, exp_avg_sq)}
-        if len(state_devs) != 1:
-            raise RuntimeError(f"params/exp_avg/exp_avg_sq must be on one device, got "
-                               f"{sorted(map(str, state_devs))}")
-        device = state_devs.pop()
-        if device.type == 'cuda':
-            others = {grads.device} | ({bf16_out.device} if bf16_out is not None else set())
-            if others != {device}:
-                raise RuntimeError(f"params/grads/states must be on one device, got "
-                                   f"{sorted(map(str, others | {device}))}")
+        arrays = [t for t in (params, grads, exp_avg, exp_avg_sq, bf16_out) if t is not None]
+        for t in arrays:
+            if t.device.type not in ('cpu', 'cuda'):
+                raise RuntimeError(f"unsupported device type: {t.device.type}")
+        # every array on the host or on one HIP device (the clip coefficient on that device)
+        gpu_devs = {t.device for t in arrays + ([clip_coef] if clip_coef is not None else []) if t.is_cuda}
+        if len(gpu_devs) > 1:
+            raise RuntimeError(f"params/grads/states must be on one device, got {sorted(map(str, gpu_devs))}")
+        if all(t.is_cuda for t in arrays):
             self._device_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
                                 grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n)
-        elif device.type == 'cpu':
-            # host state: grads and the bf16 copy may be on the host or on one device
-            gpu_devs = {t.device for t in (grads, bf16_out, clip_coef) if t is not None and t.is_cuda}
-            if len(gpu_devs) > 1:
-                raise RuntimeError(f"params/grads/states must be on one device, got {sorted(map(str, gpu_devs))}")
+        else:
             self._host_update(step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
                               grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n,
                               gpu_devs.pop() if gpu_devs else None)
-        else:
-            raise RuntimeError(f"unsupported device type: {device.type}")
 
     def _codes(self, params, grads, exp_avg):
         key = (params.dtype, grads.dtype, exp_avg.dtype)
@@ -509,8 +525,9 @@ class LayerAdam:
 
     def _host_update(self, step, lr, beta1, beta2, eps, weight_decay, bias_correction, params,
                      grads, exp_avg, exp_avg_sq, bf16_out, clip_coef, stream, n, gpu):
-        """Host state: stream it through HBM with the native chunk pipeline
-        (la_pipeline_step); returns after completion, as the reference's CPU call does."""
+        """Some arrays in host memory: stream those through HBM with the native
+        chunk pipeline (la_pipeline_step), the others are used in place on
+        ``gpu``; returns after completion, as the reference's CPU call does."""
         if not torch.cuda.is_available():
             raise RuntimeError("LayerAdam needs a HIP device (MI355X); there is no CPU arithmetic path")
         sc = self._scalars(step, lr, beta1, beta2, eps, weight_decay, bias_correction)
@@ -522,12 +539,10 @@ class LayerAdam:
             streamer = self._streamers.get(device)
             if streamer is None:
                 streamer = self._streamers[device] = HostStreamer(device)
-            g_on_host = not grads.is_cuda
-            out_on_host = bf16_out is not None and not bf16_out.is_cuda
+            on_host = _placement(params, grads, exp_avg, exp_avg_sq, bf16_out)
             self.last_stream_stats = streamer.step(
-                sc, pc, params, gc, grads, g_on_host, sc_, exp_avg, exp_avg_sq, n, bf16_out,
-                out_on_host, clip_coef, _stream_handle(stream, device),
-                synchronize=not self.overlap_host_chunks)
+                sc, pc, params, gc, grads, sc_, exp_avg, exp_avg_sq, n, bf16_out, on_host,
+                clip_coef, _stream_handle(stream, device), synchronize=not self.overlap_host_chunks)
 
     # ------------------------------------------------------------------
     # steps (layer_adam.py:270-468)

@@ -31,10 +31,11 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
-    assert L.la_abi_version() == version == 4
+    assert L.la_abi_version() == version == 5
     header = open(HEADER).read()
-    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM"):
-        value = int(re.search(rf"#define {name} \(?(-?\d+)\)?", header).group(1))
+    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
+                 "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):
+        value = int(re.search(rf"#define {name} \(?(-?\d+)u?\)?", header).group(1))
         assert getattr(_lib, name) == value, name
 
 
@@ -178,3 +179,20 @@ def test_multi_update_host_logic_without_launch():
     assert np.array_equal(vals.view(np.uint32), ref.view(np.uint32))
     assert got.step == orc.s.step == 7
     L.la_destroy(904)
+
+
+def test_pipeline_workspace_follows_the_placement():
+    """la_pipeline_workspace_bytes holds one 256-byte aligned region per
+    host-resident array and slot (chunk rounded down to 16 elements); device
+    arrays take no staging; unknown placement bits give 0."""
+    L = _lib.load()
+    F32, BF16 = _lib.LA_F32, _lib.LA_BF16
+    P, M, V, G, OUT = (_lib.LA_ON_HOST_P, _lib.LA_ON_HOST_M, _lib.LA_ON_HOST_V, _lib.LA_ON_HOST_G,
+                       _lib.LA_ON_HOST_OUT)
+    f32_region, bf16_region = 4096, 2048     # 992 elements: 3968 B and 1984 B, rounded up to 256
+    cases = {P | M | V: 3 * f32_region, P | M | V | G | OUT: 3 * f32_region + 2 * bf16_region,
+             P | G: f32_region + bf16_region, M | V: 2 * f32_region, G: bf16_region, OUT: bf16_region, 0: 0}
+    for mask, per_slot in cases.items():
+        assert L.la_pipeline_workspace_bytes(1000, 2, F32, BF16, F32, mask) == 2 * per_slot, mask
+    assert L.la_pipeline_workspace_bytes(1000, 2, F32, BF16, F32, _lib.LA_ON_HOST_ALL | 32) == 0
+    assert L.la_pipeline_workspace_bytes(15, 2, F32, BF16, F32, P) == 0

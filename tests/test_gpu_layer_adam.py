@@ -1,6 +1,8 @@
 """The LayerAdam API (drop-in for optimizer/layer_adam/layer_adam.py) on the MI355X."""
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -146,8 +148,8 @@ def test_errors(hip_device):
                          a, a, a)
     with pytest.raises(RuntimeError, match="is not supported on current hardware"):
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a.bfloat16(), a.bfloat16())
-    with pytest.raises(RuntimeError, match="one device"):
-        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a.cpu(), a, a)
+    with pytest.raises(RuntimeError, match="unsupported device type: meta"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a.to("meta"), a, a)
     with pytest.raises(RuntimeError, match="size mismatch"):
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a[:5], a, a)
 
@@ -479,6 +481,125 @@ def test_overlapped_host_chunks_in_the_runtime_protocol(pinned, hip_device):
     check()
 
 
+# which of p, m, v, g and the bf16 copy are in host memory (the rest in HBM)
+PLACEMENTS = {
+    "master+grads on host": (True, False, False, True, False),        # the runtime with moments_device
+    "master+grads+copy on host": (True, False, False, True, True),
+    "moments on host": (False, True, True, False, False),
+    "exp_avg+copy on host": (False, True, False, False, True),
+    "grads only on host": (False, False, False, True, False),
+    "copy only on host": (False, False, False, False, True),
+}
+
+
+@pytest.mark.parametrize("pinned", [True, False])
+@pytest.mark.parametrize("name", list(PLACEMENTS))
+def test_pipeline_mixed_placements_match_oracle(name, pinned, hip_device):
+    """la_pipeline_step with some arrays in host memory and the others in HBM
+    (used in place): three steps over several chunks and a scalar tail, with
+    one chunk more than the slots so that slots are reused; bit-exact with the
+    oracle; only the host-resident arrays cross the link (the byte counts);
+    page-locked and pageable (staged) host arrays."""
+    from slideformer_amd.layer_adam import HostStreamer
+    print(f"placement {name} pinned={pinned}", flush=True)
+    hp, hm, hv, hg, ho = PLACEMENTS[name]
+    n, chunk = 3 * 4096 + 4099, 4096
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + int(pinned))
+    ph = rng.normal(0, 0.02, n).astype(np.float32)
+    mh = rng.normal(0, 1e-3, n).astype(np.float32)
+    vh = np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)
+
+    def place(arr, host):
+        t = torch.from_numpy(arr.copy())
+        if host:
+            return t.pin_memory() if pinned else t
+        return t.to(hip_device)
+
+    p, m, v = place(ph, hp), place(mh, hm), place(vh, hv)
+    out = torch.empty(n, dtype=torch.bfloat16, device="cpu" if ho else hip_device)
+    if ho and pinned:
+        out = out.pin_memory()
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=chunk, slots=3)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        gb = H.to_np_bits(g, "bf16")
+        gd = (g.pin_memory() if pinned else g) if hg else g.to(hip_device)
+        adam.step_chunk(p, gd, m, v, dict(adam.defaults, step=step), bf16_out=out)
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, gb, mh, vh, g16="bf16")
+        st = adam.last_stream_stats
+        assert st.chunks == -(-n // chunk)
+        assert st.h2d_bytes == n * (4 * (hp + hm + hv) + 2 * hg)
+        assert st.d2h_bytes == n * (4 * (hp + hm + hv) + 2 * ho)
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p, "f32"), ph.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(m, "f32"), mh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(v, "f32"), vh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(ph))
+
+
+@pytest.mark.parametrize("pinned", [True, False])
+def test_moments_in_hbm_in_the_runtime_protocol(pinned, hip_device):
+    """LayerAdam(moments_device=...) under the runtime's calls
+    (transformer_layer.py:453-493): the master and the grad buffer stay in
+    host memory, add_layer_params allocates exp_avg / exp_avg_sq in HBM, and
+    each step_chunk streams only the master and the grads.  Overlapped calls
+    (overlap_host_chunks=True) of 5000 elements through a 2048 x 3 pipeline,
+    then one step_with_grad_views over the layer's parameters (one call per
+    tensor); bit-exact with the oracle after every step."""
+    from slideformer_amd.layer_adam import HostStreamer
+    sizes = [3000, 7, 9000, 1]
+    n, call = sum(sizes), 5000
+    rng = np.random.default_rng(90 + int(pinned))
+    p0 = rng.normal(0, 0.02, n).astype(np.float32)
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, overlap_host_chunks=True, moments_device=hip_device)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=2048, slots=3)
+    master = torch.from_numpy(p0.copy())
+    if pinned:
+        master = master.pin_memory()
+    views, lo = [], 0
+    for k in sizes:
+        views.append(torch.nn.Parameter(master[lo:lo + k]))
+        lo += k
+    adam.add_layer_params(0, views)
+    m, v = adam.exp_avg_flat[0], adam.exp_avg_sq_flat[0]
+    assert m.device == torch.device(hip_device) and v.device == torch.device(hip_device)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    ph, mh, vh = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+
+    def check():
+        assert np.array_equal(master.numpy().view(np.uint32), ph.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(m, "f32"), mh.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(v, "f32"), vh.view(np.uint32))
+
+    for _ in range(2):
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        if pinned:
+            g = g.pin_memory()
+        gb = H.to_np_bits(g, "bf16")
+        group = adam.begin_chunk_step(0)
+        for cs in range(0, n, call):
+            ce = min(n, cs + call)
+            adam.step_chunk(master[cs:ce], g[cs:ce], m[cs:ce], v[cs:ce], group)
+            orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[cs:ce], gb[cs:ce], mh[cs:ce],
+                       vh[cs:ce], g16="bf16")
+        adam.end_chunk_step(0)
+        check()
+    # one reference adam_update per parameter, in order (layer_adam.py:391-422), on bf16 grad views
+    g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+    gb = H.to_np_bits(g, "bf16")
+    offs = np.cumsum([0] + sizes)
+    adam.step_with_grad_views(0, {prm: g[offs[i]:offs[i + 1]] for i, prm in enumerate(views)})
+    step = adam.param_groups[0]["step"]
+    lo = 0
+    for k in sizes:
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[lo:lo + k], gb[lo:lo + k], mh[lo:lo + k],
+                   vh[lo:lo + k], g16="bf16")
+        lo += k
+    check()
+
+
 @pytest.mark.parametrize("triple", [("bf16", "bf16", "bf16"), ("f16", "f32", "f32"), ("f16", "f16", "f16")])
 def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
     """The streaming pipeline on the reference's other dtype triples: 16-bit
@@ -535,8 +656,9 @@ def test_async_pipeline_calls_with_changing_layouts(hip_device):
     chunk, slots, n, part = 1024, 3, 6 * 2600, 2600
     s_ = HostStreamer(hip_device, chunk_elems=chunk, slots=slots)
     F32, BF16 = _lib.LA_F32, _lib.LA_BF16
-    need = max(L.la_pipeline_workspace_bytes(chunk, slots, F32, gc, F32, gh, 0)
-               for gc in (F32, BF16) for gh in (0, 1))
+    STATE = _lib.LA_ON_HOST_P | _lib.LA_ON_HOST_M | _lib.LA_ON_HOST_V
+    need = max(L.la_pipeline_workspace_bytes(chunk, slots, F32, gc, F32, STATE | gh)
+               for gc in (F32, BF16) for gh in (0, _lib.LA_ON_HOST_G))
     ws = torch.empty(need + 256, dtype=torch.uint8, device=hip_device)
     wbase = (ws.data_ptr() + 255) // 256 * 256
     stg = torch.empty(need + 256, dtype=torch.uint8, pin_memory=True)
@@ -563,9 +685,9 @@ def test_async_pipeline_calls_with_changing_layouts(hip_device):
         keep.append(g)
         sc = _lib.LaScalars()
         assert L.la_scalars(81, 1, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, ctypes.byref(sc)) == 0
-        rc = L.la_pipeline_step(s_.handle, ctypes.byref(sc), F32, p[lo:hi].data_ptr(), gc, g.data_ptr(),
-                                int(on_host), F32, m[lo:hi].data_ptr(), v[lo:hi].data_ptr(), hi - lo, None, 0,
-                                None, wbase, need, st, 0, None)
+        rc = L.la_pipeline_step(s_.handle, ctypes.byref(sc), F32, p[lo:hi].data_ptr(), gc, g.data_ptr(), F32,
+                                m[lo:hi].data_ptr(), v[lo:hi].data_ptr(), hi - lo, None,
+                                STATE | (_lib.LA_ON_HOST_G if on_host else 0), None, wbase, need, st, 0, None)
         assert rc == 0, rc
         orc.update(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[lo:hi], g32 if gc == F32 else gbits, mh[lo:hi],
                    vh[lo:hi], g16="bf16" if gc == BF16 else None)
@@ -601,11 +723,12 @@ def test_host_staging_rejects_bad_buffers(hip_device):
     L.la_create(78, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0)
     sc = _lib.LaScalars()
     assert L.la_scalars(78, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.byref(sc)) == 0
-    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, False, False)
+    STATE = _lib.LA_ON_HOST_P | _lib.LA_ON_HOST_M | _lib.LA_ON_HOST_V
+    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, STATE)
     wbase = (ws.data_ptr() + 255) // 256 * 256
     st = torch.cuda.current_stream(hip_device).cuda_stream
-    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
-                            _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, wbase,
+    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(),
+                            _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, STATE, None, wbase,
                             ws.numel() - (wbase - ws.data_ptr()), st, 1, None)
     assert rc == _lib.LA_EINVAL
     assert torch.equal(p, p_before) and not m.any() and not v.any()
@@ -759,23 +882,29 @@ def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     L.la_create(77, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0)
     sc = _lib.LaScalars()
     assert L.la_scalars(77, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.byref(sc)) == 0
-    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, False, False)
+    STATE = _lib.LA_ON_HOST_P | _lib.LA_ON_HOST_M | _lib.LA_ON_HOST_V
+    ws = s.workspace(_lib.LA_F32, _lib.LA_BF16, _lib.LA_F32, STATE)
     base = (ws.data_ptr() + 255) // 256 * 256
     st = torch.cuda.current_stream(hip_device).cuda_stream
+    F32, BF16 = _lib.LA_F32, _lib.LA_BF16
+
+    def call(gptr, s_dtype=F32, on_host=STATE, out=None, ws_bytes=ws.numel() - 256, mptr=m.data_ptr()):
+        return L.la_pipeline_step(s.handle, ctypes.byref(sc), F32, p.data_ptr(), BF16, gptr, s_dtype, mptr,
+                                  v.data_ptr(), n, out, on_host, None, base, ws_bytes, st, 1, None)
+
     # (f32, bf16, bf16) is not a registered triple
-    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
-                            _lib.LA_BF16, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, ws.numel() - 256, st,
-                            1, None)
-    assert rc == _lib.LA_EDTYPE
+    assert call(g.data_ptr(), s_dtype=BF16) == _lib.LA_EDTYPE
     # a device grad pointer at an odd byte address
-    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr() + 1,
-                            0, _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, ws.numel() - 256,
-                            st, 1, None)
-    assert rc == _lib.LA_EINVAL
+    assert call(g.data_ptr() + 1) == _lib.LA_EINVAL
     # too small a workspace
-    rc = L.la_pipeline_step(s.handle, ctypes.byref(sc), _lib.LA_F32, p.data_ptr(), _lib.LA_BF16, g.data_ptr(), 0,
-                            _lib.LA_F32, m.data_ptr(), v.data_ptr(), n, None, 0, None, base, 1024, st, 1, None)
-    assert rc == _lib.LA_EINVAL
+    assert call(g.data_ptr(), ws_bytes=1024) == _lib.LA_EINVAL
+    # placement bits beyond the five arrays; a host bf16 copy without a pointer
+    assert call(g.data_ptr(), on_host=STATE | 32) == _lib.LA_EINVAL
+    assert call(g.data_ptr(), on_host=STATE | _lib.LA_ON_HOST_OUT) == _lib.LA_EINVAL
+    # a device-resident exp_avg at an address that is not a whole fp32 element
+    md = torch.zeros(n + 1, device=hip_device)
+    assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V, mptr=md.data_ptr() + 2) == _lib.LA_EINVAL
+    assert not md.any()
     torch.cuda.synchronize()
     assert torch.equal(p, p_before) and not m.any() and not v.any()
     L.la_destroy(77)

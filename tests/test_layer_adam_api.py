@@ -75,6 +75,16 @@ def test_host_tensors_without_gpu_fail_loudly():
         adam.step(0)
 
 
+def test_moments_device_is_checked_at_construction(tmp_path):
+    """moments_device must name a HIP device, and excludes the file offload
+    (which moves host-resident moments, layer_adam.py:92-106)."""
+    with pytest.raises(ValueError, match="HIP device"):
+        LayerAdam(moments_device="cpu")
+    with pytest.raises(ValueError, match="exclude each other"):
+        LayerAdam(moments_device="cuda:0", nvme_offload_fraction=0.5, offload_dir=str(tmp_path))
+    assert LayerAdam(moments_device="cuda:0").moments_device == torch.device("cuda", 0)
+
+
 def test_argument_checks_precede_dispatch():
     adam = LayerAdam()
     a = torch.zeros(10)
@@ -84,6 +94,8 @@ def test_argument_checks_precede_dispatch():
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a[:3], a, a)
     with pytest.raises(RuntimeError, match="bf16_out"):
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a, a, bf16_out=torch.zeros(10))
+    with pytest.raises(RuntimeError, match="unsupported device type: meta"):
+        adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a.to("meta"), a)
 
 
 def test_disk_offloader_round_trip(tmp_path):
