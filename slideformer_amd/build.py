@@ -1,6 +1,7 @@
 """Build recipe for the in-tree HIP library ``slideformer_amd/lib/libslideformer_amd.so``.
 
-Usage: ``python -m slideformer_amd.build`` (also called by ``__graft_entry__.build()``).
+Usage: ``python -m slideformer_amd.build`` (also called by ``__graft_entry__.build()``);
+it also writes the small-grid test build ``lib/libslideformer_amd_smallgrid.so``.
 
 The library is one HIP translation unit compiled for gfx950 only.  Flags:
   -ffp-contract=off       every FMA in the kernels is an explicit fmaf(), so the
@@ -64,5 +65,21 @@ def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: boo
     return out
 
 
+# A build with tiny grid caps, loaded only by the GPU tests: the update kernel's
+# grid-stride loop (taken by the product build only above 2^34 elements per
+# call), the own-launch path of la_adam_update_multi for small segments and
+# the grad norm's many-trip loop then run at test sizes.  Same sources, same
+# flags; only these launch limits differ.
+SMALL_GRID_LIB = os.path.join(LIB_DIR, "libslideformer_amd_smallgrid.so")
+SMALL_GRID_DEFINES = {"LA_MAX_GRID": 64, "LA_NORM_MAX_GRID": 2, "LA_MULTI_OWN_LAUNCH_RUNS": 8}
+
+
+def build_all(verbose: bool = False) -> list:
+    """The product library and the small-grid test build."""
+    return [build_library(verbose=verbose),
+            build_library(out=SMALL_GRID_LIB, defines=SMALL_GRID_DEFINES, verbose=verbose)]
+
+
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    for path in build_all(verbose=True):
+        print(path)

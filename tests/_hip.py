@@ -30,11 +30,28 @@ def to_np_bits(t: torch.Tensor, kind: str) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16).copy()
 
 
+_small_grid = None
+
+
+def load_small_grid():
+    """The small-grid test build of the library (slideformer_amd.build.SMALL_GRID_LIB),
+    loaded beside the product build; raises if it has not been built."""
+    global _small_grid
+    if _small_grid is None:
+        import os
+
+        from slideformer_amd.build import SMALL_GRID_LIB
+        if not os.path.exists(SMALL_GRID_LIB):
+            raise ImportError(f"{SMALL_GRID_LIB} not built; run `python -m slideformer_amd.build`")
+        _small_grid = _lib._declare(ctypes.CDLL(SMALL_GRID_LIB))
+    return _small_grid
+
+
 class HipAdam:
     """One optimizer id of the HIP library, called through the C-ABI."""
 
-    def __init__(self, lr, betas, eps, wd, adamw):
-        self.L = _lib.load()
+    def __init__(self, lr, betas, eps, wd, adamw, *, lib=None):
+        self.L = lib if lib is not None else _lib.load()
         self.id = next(_ids)
         _lib.check(self.L.la_create(self.id, lr, betas[0], betas[1], eps, wd, int(adamw), 0), "la_create")
 

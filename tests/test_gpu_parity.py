@@ -490,3 +490,92 @@ def test_multi_update_equals_separate_calls(triple, mode, hip_device):
         assert np.array_equal(H.to_np_bits(a[k][0], pk), hp[k]), k
         assert np.array_equal(H.to_np_bits(a[k][2], sk), hm[k]), k
         assert np.array_equal(H.to_np_bits(a[k][3], sk), hv[k]), k
+
+
+# ---------------------------------------------------------------------------
+# launch paths the product build takes only at sizes beyond one GPU: the
+# small-grid test build (64 waves per update launch, 2 workgroups per norm
+# launch, own launches from 8 runs per segment) against the product build
+# ---------------------------------------------------------------------------
+
+SMALL_GRID_SIZES = [7, 16, 64 * 256 * 3 + 5, 64 * 256 * 40 + 13, 1_000_003]
+
+
+@pytest.mark.parametrize("triple", [("f32", "bf16", "f32"), ("bf16", "bf16", "bf16"), ("f16", "f16", "f32")])
+def test_grid_stride_update_equals_one_shot(triple, hip_device):
+    """The update kernel's grid-stride loop (several trips of 64 waves) and its
+    scalar head/tail loop, in the small-grid build, give the same bits as the
+    product build's one-shot grid, with a bf16 copy and a clip coefficient,
+    over three steps; the multi-segment entry point likewise, with every
+    segment of 2048 or more elements on its own grid-stride launch.  The
+    product build is itself pinned to the oracle by the tests above; the
+    small-grid results are also checked against the oracle here."""
+    pk, gk, sk = triple
+    log(f"grid-stride update {triple}")
+    small = H.load_small_grid()
+    coef = torch.tensor([0.61], device=hip_device)
+
+    def make(seed):
+        torch.manual_seed(seed)
+        out = []
+        for n in SMALL_GRID_SIZES:
+            off = n % 3                                        # element offsets inside a larger buffer
+            def buf(dt, std):
+                return (torch.randn(n + 4, device=hip_device) * std).to(H.TD[dt])[off:off + n]
+            # every stream at the same element offset: the vector path, not the all-scalar one
+            out.append([buf(pk, 0.02), buf(gk, 1e-3), buf(sk, 1e-3), buf(sk, 1e-3).abs_(),
+                        torch.empty(n + 4, dtype=torch.bfloat16, device=hip_device)[off:off + n]])
+        return out
+
+    for multi in (False, True):
+        a, b = make(5), make(5)
+        opt_a = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True, lib=small)
+        opt_b = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+        for step in (1, 2, 3):
+            if multi:
+                opt_a.update_multi(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, a, coef=coef)
+                opt_b.update_multi(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, b, coef=coef)
+            else:
+                for (p, g, m, v, o), (q, h, mm, vv, oo) in zip(a, b):
+                    opt_a.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, out=o, coef=coef)
+                    opt_b.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, q, h, mm, vv, out=oo, coef=coef)
+        torch.cuda.synchronize()
+        for k, (sa, sb) in enumerate(zip(a, b)):
+            for i, kind in ((0, pk), (2, sk), (3, sk), (4, "bf16")):
+                assert np.array_equal(H.to_np_bits(sa[i], kind), H.to_np_bits(sb[i], kind)), (multi, k, i)
+    # against the oracle, replaying the same five calls per step in order: the
+    # beta-power state takes the multiply path on a step's first call and the
+    # pow path on the others (cpu_adam.h:57-89), which changes step_size bits
+    host = [[H.to_np_bits(t, kind) for t, kind in zip(seg[:4], (pk, gk, sk, sk))] for seg in make(5)]
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        for p, g, m, v in host:
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, _view(p, pk), _view(g, gk), _view(m, sk),
+                       _view(v, sk), p16=KIND16[pk], g16=KIND16[gk], s16=KIND16[sk], clip_coef=0.61)
+    for k, (p, g, m, v) in enumerate(host):
+        assert np.array_equal(H.to_np_bits(a[k][0], pk), p), k
+        assert np.array_equal(H.to_np_bits(a[k][2], sk), m), k
+        assert np.array_equal(H.to_np_bits(a[k][3], sk), v), k
+
+
+@pytest.mark.parametrize("gk", ["bf16", "f32", "f16"])
+def test_grad_norm_with_two_workgroups(gk, hip_device):
+    """The grad norm's stage 1 with a two-workgroup grid (many trips of the
+    unrolled loop, then its remainder and the head/tail elements) stays within
+    1e-12 of the oracle's compensated float64 sum, at sizes around one trip."""
+    import ctypes
+
+    small = H.load_small_grid()
+    log(f"two-workgroup norm {gk}")
+    trip = 2 * 512 * 8 * 4                                     # elements per trip of the unrolled loop
+    for n in (1, 3, trip - 1, trip, trip + 5, 7 * trip + 1001, 1_000_003):
+        g = (torch.randn(n + 2, device=hip_device) * 1e-2).to(H.TD[gk])[1:1 + n]
+        ws = torch.zeros(small.la_grad_sqnorm_workspace(n) // 8 + 1, dtype=torch.float64, device=hip_device)
+        assert small.la_grad_sqnorm_workspace(n) <= 2 * 8
+        out = torch.zeros(1, dtype=torch.float64, device=hip_device)
+        rc = small.la_grad_sqnorm(H.CODE[gk], ctypes.c_void_p(g.data_ptr()), n, ctypes.c_void_p(ws.data_ptr()),
+                                  ws.numel() * 8, ctypes.c_void_p(out.data_ptr()), 0,
+                                  torch.cuda.current_stream(hip_device).cuda_stream)
+        assert rc == 0
+        exact = O.grad_sqnorm(_view(H.to_np_bits(g, gk), gk), KIND16[gk])
+        assert abs(out.item() - exact) <= 1e-12 * exact, (n, out.item(), exact)
