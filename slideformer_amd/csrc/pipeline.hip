@@ -425,13 +425,14 @@ try {
     // of staged calls that return once queued (one per 32 Mi elements) stalled
     // the copy streams for ~3.5 ms per Llama-3.1-8B layer, twice; without
     // them the series runs at the single-call rate.
+    // Otherwise only the H2D stream waits: the update of chunk i waits for
+    // ev_h2d of chunk i and the copy-back for ev_comp, so the other two streams
+    // follow the caller's work through those events.
     LA_STEP_TRY(hipEventRecord(pl->t_begin, caller));
     if (staged) {
         LA_STEP_TRY(hipEventSynchronize(pl->t_begin));
     } else {
         LA_STEP_TRY(hipStreamWaitEvent(pl->h2d, pl->t_begin, 0));
-        LA_STEP_TRY(hipStreamWaitEvent(pl->comp, pl->t_begin, 0));
-        LA_STEP_TRY(hipStreamWaitEvent(pl->d2h, pl->t_begin, 0));
     }
     LA_STEP_TRY(hipEventRecord(pl->t_comp_begin, pl->comp));
     LA_STEP_TRY(hipEventRecord(pl->t_d2h_begin, pl->d2h));
