@@ -281,6 +281,11 @@ class LayerAdam:
             adamw_mode=adamw_mode,
         )
         self.param_groups = []
+        if moments_device is not None and torch.device(moments_device).type != 'cuda':
+            raise ValueError(f"moments_device must be a HIP device, got {moments_device}")
+        if moments_device is not None and nvme_offload_fraction > 0.0:
+            raise ValueError("moments_device and nvme_offload_fraction > 0 exclude each other: "
+                             "the file offload moves host-resident moments")
 
         # The reference loads its CPU extension here (layer_adam.py:59); this
         # loads the HIP library and fails loudly if it is missing.
@@ -298,11 +303,6 @@ class LayerAdam:
         self.pin_host_state = pin_host_state
         self.overlap_host_chunks = overlap_host_chunks
         self.moments_device = torch.device(moments_device) if moments_device is not None else None
-        if self.moments_device is not None and self.moments_device.type != 'cuda':
-            raise ValueError(f"moments_device must be a HIP device, got {self.moments_device}")
-        if self.moments_device is not None and nvme_offload_fraction > 0.0:
-            raise ValueError("moments_device and nvme_offload_fraction > 0 exclude each other: "
-                             "the file offload moves host-resident moments")
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
         assert 0.0 <= nvme_offload_fraction <= 1.0
@@ -342,10 +342,13 @@ class LayerAdam:
             except Exception:
                 pass
         if getattr(self, 'offloader', None) is not None:
+            # layer_adam.py:117-124 removes every "offload-*" file of the
+            # directory, those of other processes sharing it included; the
+            # files here carry the process id, and only this process's go
             del self.offloader
             if self.offload_dir and os.path.exists(self.offload_dir):
                 try:
-                    for file in glob.glob(os.path.join(self.offload_dir, "offload-*")):
+                    for file in glob.glob(os.path.join(self.offload_dir, f"offload-{os.getpid()}-*")):
                         os.remove(file)
                 except OSError:
                     pass

@@ -168,3 +168,23 @@ def test_torch_adam_update_formula():
     adam.torch_adam_update(data, grad, m, v, 0.1, 0.9, 0.999, 1e-8, 0.1, 1 - 0.9, 1 - 0.999)
     expected = 1.0 * (1 - 0.1 * 0.1) - 0.1 * 1.0
     torch.testing.assert_close(data, torch.full((4,), expected), rtol=1e-5, atol=1e-6)
+
+
+def test_offload_cleanup_leaves_other_processes_files(tmp_path):
+    """Tearing LayerAdam down removes this process's offload files and no
+    other process's (the reference removes every "offload-*" file of the
+    directory, layer_adam.py:117-124)."""
+    import gc
+    import os
+
+    foreign = tmp_path / "offload-999999999-7"
+    foreign.write_bytes(b"another run's moments")
+    adam = LayerAdam(nvme_offload_fraction=1.0, offload_dir=str(tmp_path), num_layer=2)
+    for i in range(2):
+        adam.add_layer_params(i, [torch.nn.Parameter(torch.randn(100))])
+    adam.offloader.sync_write_events()
+    assert list(tmp_path.glob(f"offload-{os.getpid()}-*"))
+    del adam
+    gc.collect()
+    assert list(tmp_path.glob(f"offload-{os.getpid()}-*")) == []
+    assert foreign.read_bytes() == b"another run's moments"
