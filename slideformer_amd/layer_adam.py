@@ -748,8 +748,10 @@ class GradNormAccumulator:
 
     One accumulator is one running sum: its ``add`` and ``finish`` calls must be
     ordered, i.e. on one stream or synchronised between streams.  Its scratch
-    is allocated once, at the size any buffer needs, so it is never freed while
-    a launch may still use it."""
+    is allocated once, at the size any buffer needs, and is marked as used by
+    every stream a launch runs on (``record_stream``), so that the caching
+    allocator does not hand it out again before those launches are done, even
+    if the accumulator is dropped early."""
 
     def __init__(self, device):
         self.lib = _lib.load()
@@ -767,20 +769,26 @@ class GradNormAccumulator:
         if grad.dtype not in _DTYPE_CODE:
             raise RuntimeError(f"unsupported grad dtype {grad.dtype}")
         with torch.cuda.device(self.device):
+            s = _torch_stream(stream, self.device)
             _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[grad.dtype], _ptr(grad), grad.numel(),
                                                _ptr(self.work), self.work.numel() * 8, _ptr(self.sqnorm),
-                                               int(self.count > 0), _stream_handle(stream, self.device)),
+                                               int(self.count > 0), s.cuda_stream),
                        "la_grad_sqnorm")
+            self.work.record_stream(s)
+            self.sqnorm.record_stream(s)
         self.count += 1
 
     @torch.no_grad()
     def finish(self, max_norm: float, *, stream=None):
-        """``(coef, norm)`` as fp32 device scalars; no host synchronisation."""
-        coef = torch.empty(1, dtype=torch.float32, device=self.device)
-        norm = torch.empty(1, dtype=torch.float32, device=self.device)
+        """``(coef, norm)`` as fp32 device scalars, allocated on the stream that
+        writes them; no host synchronisation."""
         with torch.cuda.device(self.device):
-            handle = _stream_handle(stream, self.device)
+            s = _torch_stream(stream, self.device)
+            with torch.cuda.stream(s):
+                coef = torch.empty(1, dtype=torch.float32, device=self.device)
+                norm = torch.empty(1, dtype=torch.float32, device=self.device)
             # with nothing added, sqnorm is still the zero it was created as: coef = 1
             _lib.check(self.lib.la_clip_coef(_ptr(self.sqnorm), float(max_norm), _ptr(coef), _ptr(norm),
-                                             handle), "la_clip_coef")
+                                             s.cuda_stream), "la_clip_coef")
+            self.sqnorm.record_stream(s)
         return coef, norm

@@ -759,6 +759,34 @@ def test_clip_grad_norm_on_two_streams_at_once(hip_device):
             assert r[ci].item() == np.float32(c_ref) and r[ni].item() == np.float32(n_ref)
 
 
+def test_grad_norm_accumulator_on_side_streams(hip_device):
+    """GradNormAccumulator driven on side streams (a torch stream, then a raw
+    handle), dropped right after finish(): its scratch is recorded on those
+    streams, so allocations made meanwhile on the current stream do not take it
+    over; the coefficient equals the oracle's."""
+    rng = np.random.default_rng(33)
+    grads = [torch.from_numpy(rng.normal(0, 1e-2, k).astype(np.float32)).bfloat16().to(hip_device)
+             for k in (3_000_001, 5, 400_000)]
+    adam = LayerAdam()
+    side = torch.cuda.Stream(device=hip_device)
+    side.wait_stream(torch.cuda.current_stream(hip_device))
+    outs = []
+    for rep in range(3):
+        acc = adam.grad_norm_begin(hip_device)
+        for i, g in enumerate(grads):
+            acc.add(g, stream=side if i % 2 == 0 else side.cuda_stream)
+        outs.append(acc.finish(1.0, stream=side))
+        del acc
+        # allocations on the current stream while the side stream may still run
+        junk = [torch.full((1 << 16,), 7.0, dtype=torch.float64, device=hip_device) for _ in range(8)]
+        del junk
+    torch.cuda.synchronize()
+    sq = sum(O.grad_sqnorm(H.to_np_bits(g, "bf16"), "bf16") for g in grads)
+    c_ref, n_ref = O.clip_coef(sq, 1.0)
+    for coef, norm in outs:
+        assert coef.item() == np.float32(c_ref) and norm.item() == np.float32(n_ref)
+
+
 def test_launch_status_ignores_an_earlier_unrelated_error(hip_device):
     """A HIP error left in the thread by an unrelated host call (here a failed
     hipSetDevice) is not reported as a failure of the next launch.  Only
