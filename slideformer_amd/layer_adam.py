@@ -190,29 +190,39 @@ def _unsupported(p, g, s) -> RuntimeError:
         f"and state type {_DTYPE_NAME.get(s, s)} is not supported on current hardware")
 
 
-def _batchable(entries) -> bool:
-    """True when the (params, grads, exp_avg, exp_avg_sq) tensors can go to
-    la_adam_update_multi: one HIP device, one registered dtype triple, contiguous,
-    matching sizes, and no two tensors written by the update overlap."""
+def _segments(entries):
+    """The la_segment_t array of one la_adam_update_multi call over the
+    (params, grads, exp_avg, exp_avg_sq) entries, or None when they cannot go
+    in one: one HIP device, one registered dtype triple, contiguous, matching
+    sizes, and no two tensors written by the update overlapping.  One pass;
+    the array is built as six uint64 per segment (the layout of la_segment_t:
+    p, g, m, v, p_bf16_out, n)."""
     p0, g0, m0, _ = entries[0]
-    if p0.device.type != 'cuda':
-        return False
-    key = (p0.dtype, g0.dtype, m0.dtype)
-    if key not in SUPPORTED_TRIPLES:
-        return False
-    spans = []
+    if not p0.is_cuda:
+        return None
+    pdt, gdt, sdt = p0.dtype, g0.dtype, m0.dtype
+    if (pdt, gdt, sdt) not in SUPPORTED_TRIPLES:
+        return None
+    dev = p0.get_device()
+    pe, se = p0.element_size(), m0.element_size()
+    flat, spans = [], []
     for p, g, m, v in entries:
         n = p.numel()
-        for t in (p, g, m, v):
-            if t.device != p0.device or not t.is_contiguous() or t.numel() != n:
-                return False
-        if (p.dtype, g.dtype, m.dtype) != key or v.dtype != m.dtype:
-            return False
-        for t in (p, m, v):
-            if n:
-                spans.append((t.data_ptr(), t.data_ptr() + n * t.element_size()))
+        if (g.numel() != n or m.numel() != n or v.numel() != n
+                or p.dtype != pdt or g.dtype != gdt or m.dtype != sdt or v.dtype != sdt
+                or not (p.is_contiguous() and g.is_contiguous() and m.is_contiguous() and v.is_contiguous())
+                or p.get_device() != dev or g.get_device() != dev or m.get_device() != dev
+                or v.get_device() != dev):
+            return None
+        pp, mp, vp = p.data_ptr(), m.data_ptr(), v.data_ptr()
+        flat += (pp, g.data_ptr(), mp, vp, 0, n)
+        if n:
+            spans += ((pp, pp + n * pe), (mp, mp + n * se), (vp, vp + n * se))
     spans.sort()
-    return all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+    for a, b in zip(spans, spans[1:]):
+        if a[1] > b[0]:
+            return None
+    return ctypes.cast((ctypes.c_uint64 * len(flat))(*flat), ctypes.POINTER(_lib.LaSegment))
 
 
 def _torch_stream(stream, device):
@@ -567,11 +577,12 @@ class LayerAdam:
             param_group['step'] += 1
             entries = []
             for p in param_group['params']:
-                if p.grad is None:
+                g = p.grad
+                if g is None:
                     continue
                 state = self.state[p]
-                assert p.data.numel() == p.grad.data.numel(), "params and grads must have the same size"
-                entries.append((p.data, p.grad.data, state['exp_avg'], state['exp_avg_sq']))
+                assert p.numel() == g.numel(), "params and grads must have the same size"
+                entries.append((p, g, state['exp_avg'], state['exp_avg_sq']))
             self._update_tensors(param_group, entries)
         self.synchronize()
         self._post_step(layer_idx)
@@ -600,8 +611,8 @@ class LayerAdam:
                     print(f"Warning: no grad view for parameter {p}, skipping update")
                     continue
                 state = self.state[p]
-                assert p.data.numel() == grad.numel(), "params and grads must have the same size"
-                entries.append((p.data, grad, state['exp_avg'], state['exp_avg_sq']))
+                assert p.numel() == grad.numel(), "params and grads must have the same size"
+                entries.append((p, grad, state['exp_avg'], state['exp_avg_sq']))
             self._update_tensors(param_group, entries)
         self.synchronize()
         self._post_step(layer_idx)
@@ -626,13 +637,9 @@ class LayerAdam:
         beta1, beta2 = param_group['betas']
         hp = (param_group['step'], param_group['lr'], beta1, beta2, param_group['eps'],
               param_group['weight_decay'], param_group['bias_correction'])
-        if len(entries) > 1 and _batchable(entries):
+        segs = _segments(entries) if len(entries) > 1 else None
+        if segs is not None:
             p0, g0, m0, _ = entries[0]
-            segs = (_lib.LaSegment * len(entries))()
-            for k, (p, g, m, v) in enumerate(entries):
-                segs[k].p, segs[k].g, segs[k].m, segs[k].v = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
-                segs[k].p_bf16_out = None
-                segs[k].n = p.numel()
             with torch.cuda.device(p0.device):
                 rc = self.lib.la_adam_update_multi(
                     self.optimizer_id, int(hp[0]), hp[1], hp[2], hp[3], hp[4], hp[5], int(bool(hp[6])),

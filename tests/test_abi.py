@@ -196,3 +196,16 @@ def test_pipeline_workspace_follows_the_placement():
         assert L.la_pipeline_workspace_bytes(1000, 2, F32, BF16, F32, mask) == 2 * per_slot, mask
     assert L.la_pipeline_workspace_bytes(1000, 2, F32, BF16, F32, _lib.LA_ON_HOST_ALL | 32) == 0
     assert L.la_pipeline_workspace_bytes(15, 2, F32, BF16, F32, P) == 0
+
+
+def test_segment_layout_is_six_words():
+    """LayerAdam builds la_segment_t arrays as six uint64 per segment
+    (p, g, m, v, p_bf16_out, n); the struct must have exactly that layout."""
+    S = _lib.LaSegment
+    assert ctypes.sizeof(S) == 48
+    assert [getattr(S, f).offset for f in ("p", "g", "m", "v", "p_bf16_out", "n")] == [0, 8, 16, 24, 32, 40]
+    header = open(HEADER).read()
+    body = re.search(r"typedef struct \{([^}]*)\} la_segment_t;", header).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = re.findall(r"(\w+);", body)
+    assert names == ["p", "g", "m", "v", "p_bf16_out", "n"]
