@@ -14,23 +14,27 @@ from tests import _hip as H
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("where", ["device", "host"])
 @pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
-def test_known_answer_vs_torch_adamw(gdtype, hip_device):
+def test_known_answer_vs_torch_adamw(gdtype, where, hip_device):
     """The reference's only numeric test, test_shared_data_parallel.py:53-93, single
-    process: sizes (19, 3, 0) in chunks of 5, five steps, lr change at step 3."""
+    process: sizes (19, 3, 0) in chunks of 5, five steps, lr change at step 3.
+    The reference calls step_chunk on CPU tensors (:70-73); "host" does the
+    same here (streamed through HBM), "device" keeps everything in HBM."""
     adam = LayerAdam(lr=0.01, betas=(0.8, 0.95), eps=1e-6, weight_decay=0.1)
     chunk = 5
+    at = hip_device if where == "device" else "cpu"
     for layer, size in enumerate((19, 3, 0)):
         initial = torch.linspace(-0.5, 0.5, size)
-        params = initial.clone().to(hip_device)
-        first = torch.zeros(size, device=hip_device)
-        second = torch.zeros(size, device=hip_device)
+        params = initial.clone().to(at)
+        first = torch.zeros(size, device=at)
+        second = torch.zeros(size, device=at)
         reference = torch.nn.Parameter(initial.clone())
         tadam = torch.optim.AdamW([reference], lr=0.01, betas=(0.8, 0.95), eps=1e-6,
                                   weight_decay=0.1, foreach=False)
         for step in range(1, 6):
             grads = ((torch.arange(size) * 0.13 + step * 0.2).sin() * 0.1).to(gdtype)
-            gd = grads.to(hip_device)
+            gd = grads.to(at)
             lr = 0.01 if step < 3 else 0.003
             tadam.param_groups[0]["lr"] = lr
             for start in range(0, size, chunk):
