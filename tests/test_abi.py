@@ -209,3 +209,52 @@ def test_segment_layout_is_six_words():
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
     names = re.findall(r"(\w+);", body)
     assert names == ["p", "g", "m", "v", "p_bf16_out", "n"]
+
+
+def test_state_machine_is_safe_under_concurrent_calls():
+    """The beta-power state of one id is guarded by a mutex: 8 threads call
+    la_scalars for the same step at once, 150 steps in a row (ctypes releases
+    the GIL, so the calls really overlap).  Per step exactly one call takes the
+    multiply path (the first one to hold the state) and the other seven the
+    pow path (cpu_adam.h:57-89), each bit-exact with the oracle replaying that
+    order; nothing tears."""
+    import threading
+
+    L = _lib.load()
+    threads, steps = 8, 150
+    L.la_create(905, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0)
+    barrier = threading.Barrier(threads)
+    got = [[None] * steps for _ in range(threads)]
+
+    def worker(t):
+        for st in range(1, steps + 1):
+            barrier.wait()
+            sc = _scalars(L, 905, st, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+            got[t][st - 1] = (np.float32(sc.beta1_t), np.float32(sc.beta2_t), np.float32(sc.step_size),
+                              np.float32(sc.bias_correction2), sc.step)
+
+    ws = [threading.Thread(target=worker, args=(t,)) for t in range(threads)]
+    for w in ws:
+        w.start()
+    for w in ws:
+        w.join()
+    L.la_destroy(905)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    lib = O.lib()
+    for st in range(1, steps + 1):
+        expected = []
+        for k in range(threads):                     # the order the lock admits them in
+            lib.orc_increment_step(orc.s, st, 0.9, 0.999)
+            lib.orc_update_state(orc.s, 1e-3, 1e-8, 0.01, 1)
+            r = orc.scalars()
+            expected.append((r[0], r[1], r[4], r[3], st))
+        first, rest = expected[0], expected[1]
+        assert all(e == rest for e in expected[1:])
+        outs = [got[t][st - 1] for t in range(threads)]
+        n_first = sum(o[:4] == first[:4] for o in outs)
+        n_rest = sum(o[:4] == rest[:4] for o in outs)
+        if first[:4] == rest[:4]:
+            assert n_first == threads, st
+        else:
+            assert (n_first, n_rest) == (1, threads - 1), (st, outs, first, rest)
+        assert all(o[4] == st for o in outs)
