@@ -258,3 +258,35 @@ def test_state_machine_is_safe_under_concurrent_calls():
         else:
             assert (n_first, n_rest) == (1, threads - 1), (st, outs, first, rest)
         assert all(o[4] == st for o in outs)
+
+
+def test_header_is_usable_from_c(tmp_path):
+    """tests/native/abi_from_c.c, compiled as C11 with -Wall -Werror against
+    include/layer_adam.h and linked to the library, calls the host-side entry
+    points; its beta-power scalars match the CPU checker bit for bit."""
+    import os
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = os.path.join(os.path.dirname(__file__), "native", "abi_from_c.c")
+    exe = str(tmp_path / "abi_from_c")
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", os.path.dirname(HEADER),
+                    src, "-L", libdir, "-lslideformer_amd", f"-Wl,-rpath,{libdir}", "-o", exe], check=True)
+    res = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, (res.returncode, res.stderr)
+    lines = res.stdout.split("\n")[:7]
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    lib = O.lib()
+    for st, line in zip((1, 2, 3, 4, 5, 5, 9), lines):
+        lib.orc_increment_step(orc.s, st, 0.9, 0.999)
+        lib.orc_update_state(orc.s, 1e-3, 1e-8, 0.01, 1)
+        r = orc.scalars()    # b1t, b2t, bc1, bc2, step_size, w_decay, ...
+        f = line.split()
+        assert int(f[0]) == st
+        got = np.array([float.fromhex(x) for x in f[1:7]], dtype=np.float32)
+        assert np.array_equal(got.view(np.uint32), r[:6].view(np.uint32)), (st, got, r[:6])
+        assert int(f[7]) == 2
