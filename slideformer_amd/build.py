@@ -1,7 +1,8 @@
 """Build recipe for the in-tree HIP library ``slideformer_amd/lib/libslideformer_amd.so``.
 
 Usage: ``python -m slideformer_amd.build`` (also called by ``__graft_entry__.build()``);
-it also writes the small-grid test build ``lib/libslideformer_amd_smallgrid.so``.
+it also writes the small-grid test build ``lib/libslideformer_amd_smallgrid.so`` and the
+C test driver ``tests/native/_build/device_from_c``.
 
 The library is one HIP translation unit compiled for gfx950 only.  Flags:
   -ffp-contract=off       every FMA in the kernels is an explicit fmaf(), so the
@@ -74,10 +75,39 @@ SMALL_GRID_LIB = os.path.join(LIB_DIR, "libslideformer_amd_smallgrid.so")
 SMALL_GRID_DEFINES = {"LA_MAX_GRID": 64, "LA_NORM_MAX_GRID": 2, "LA_MULTI_OWN_LAUNCH_RUNS": 8}
 
 
+# A plain C program that runs the step on the GPU through the C-ABI alone
+# (HIP runtime API for memory, no torch); run by the GPU tests.
+C_DRIVER_SRC = os.path.join(REPO_DIR, "tests", "native", "device_from_c.c")
+C_DRIVER = os.path.join(REPO_DIR, "tests", "native", "_build", "device_from_c")
+
+
+def build_c_driver(verbose: bool = False) -> str:
+    """Compile tests/native/device_from_c.c as C11 with gcc against the header and the library."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        raise RuntimeError("gcc not found")
+    os.makedirs(os.path.dirname(C_DRIVER), exist_ok=True)
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
+    cmd = [gcc, "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(REPO_DIR, "include"), "-I", os.path.join(rocm, "include"), C_DRIVER_SRC,
+           "-L", LIB_DIR, "-lslideformer_amd", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN/../../../slideformer_amd/lib", f"-Wl,-rpath,{os.path.join(rocm, 'lib')}",
+           "-o", C_DRIVER + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"gcc failed with code {res.returncode}")
+    os.replace(C_DRIVER + ".tmp", C_DRIVER)
+    return C_DRIVER
+
+
 def build_all(verbose: bool = False) -> list:
-    """The product library and the small-grid test build."""
+    """The product library, the small-grid test build and the C test driver."""
     return [build_library(verbose=verbose),
-            build_library(out=SMALL_GRID_LIB, defines=SMALL_GRID_DEFINES, verbose=verbose)]
+            build_library(out=SMALL_GRID_LIB, defines=SMALL_GRID_DEFINES, verbose=verbose),
+            build_c_driver(verbose=verbose)]
 
 
 if __name__ == "__main__":

@@ -579,3 +579,47 @@ def test_grad_norm_with_two_workgroups(gk, hip_device):
         assert rc == 0
         exact = O.grad_sqnorm(_view(H.to_np_bits(g, gk), gk), KIND16[gk])
         assert abs(out.item() - exact) <= 1e-12 * exact, (n, out.item(), exact)
+
+
+# ---------------------------------------------------------------------------
+# the C-ABI from a plain C program (no torch, no Python in the process)
+# ---------------------------------------------------------------------------
+
+def test_plain_c_program_runs_the_step(tmp_path):
+    """tests/native/device_from_c.c (built by slideformer_amd.build) computes the
+    clip coefficient and three clipped AdamW steps with the bf16 copy through
+    include/layer_adam.h and the HIP runtime API alone; every output bit
+    equals the oracle's."""
+    import os
+    import subprocess
+
+    from slideformer_amd.build import C_DRIVER
+    assert os.path.exists(C_DRIVER), "run `python -m slideformer_amd.build` first"
+    n = 100_003
+    rng = np.random.default_rng(404)
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    g = O.f32_to_bf16(rng.normal(0, 1e-2, n).astype(np.float32))
+    m = rng.normal(0, 1e-3, n).astype(np.float32)
+    v = np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)
+    src, dst = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(src, "wb") as f:
+        f.write(np.uint64(n).tobytes() + p.tobytes() + g.tobytes() + m.tobytes() + v.tobytes())
+    log(f"device_from_c n={n}")
+    res = subprocess.run([C_DRIVER, str(src), str(dst)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, (res.returncode, res.stderr)
+    raw = np.fromfile(dst, dtype=np.uint8)
+    coef, norm = np.frombuffer(raw[:8].tobytes(), dtype=np.float32)
+    body = raw[8:]
+    gp = np.frombuffer(body[:4 * n].tobytes(), dtype=np.float32)
+    gm = np.frombuffer(body[4 * n:8 * n].tobytes(), dtype=np.float32)
+    gv = np.frombuffer(body[8 * n:12 * n].tobytes(), dtype=np.float32)
+    gout = np.frombuffer(body[12 * n:14 * n].tobytes(), dtype=np.uint16)
+    c_ref, n_ref = O.clip_coef(O.grad_sqnorm(g, "bf16"), 0.5)
+    assert coef == np.float32(c_ref) and norm == np.float32(n_ref) and coef < 1.0
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, g16="bf16", clip_coef=float(coef))
+    assert np.array_equal(gp.view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(gm.view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(gv.view(np.uint32), v.view(np.uint32))
+    assert np.array_equal(gout, O.f32_to_bf16(p))
