@@ -266,6 +266,7 @@ class LayerAdam:
             pin_host_state: bool = False,
             overlap_host_chunks: bool = False,
             moments_device: Optional[torch.device] = None,
+            moments_hbm_bytes: Optional[int] = None,
     ):
         """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
         ``device``: the HIP device that updates host-resident state (default: current);
@@ -274,6 +275,10 @@ class LayerAdam:
         reference does).  With a host-resident master (the runtime's layout) the
         moments then stay in HBM and each step moves 6 B/param to the device
         and 4 B/param back instead of 14 and 12;
+        ``moments_hbm_bytes``: with ``moments_device``, the most HBM the moments
+        may take (None = no limit); layers registered once it is used up keep
+        their moments beside their params, so a model whose moments do not all
+        fit in HBM keeps as many layers' moments there as the budget allows;
         ``pin_host_state``: allocate host-resident moments in page-locked memory
         (streamed without staging copies; the reference allocates pageable memory,
         which the pipeline stages through page-locked buffers);
@@ -296,6 +301,8 @@ class LayerAdam:
         if moments_device is not None and nvme_offload_fraction > 0.0:
             raise ValueError("moments_device and nvme_offload_fraction > 0 exclude each other: "
                              "the file offload moves host-resident moments")
+        if moments_hbm_bytes is not None and (moments_device is None or moments_hbm_bytes < 0):
+            raise ValueError("moments_hbm_bytes needs moments_device and must be >= 0")
 
         # The reference loads its CPU extension here (layer_adam.py:59); this
         # loads the HIP library and fails loudly if it is missing.
@@ -313,6 +320,8 @@ class LayerAdam:
         self.pin_host_state = pin_host_state
         self.overlap_host_chunks = overlap_host_chunks
         self.moments_device = torch.device(moments_device) if moments_device is not None else None
+        self.moments_hbm_bytes = moments_hbm_bytes
+        self.moments_hbm_used = 0     # bytes of moments placed on moments_device so far
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
         assert 0.0 <= nvme_offload_fraction <= 1.0
@@ -370,11 +379,18 @@ class LayerAdam:
         return sum(p.numel() for p in self.param_groups[layer_idx]['params'])
 
     def add_layer_params(self, layer_idx: int, params: Iterable[torch.nn.Parameter]) -> int:
-        """Register one layer; allocate its flat m/v beside the params (layer_adam.py:134-198)."""
+        """Register one layer; allocate its flat m/v beside the params (layer_adam.py:134-198),
+        or on ``moments_device`` while its budget allows."""
         params = list(params)
         if not params:
             return -1
-        device = self.moments_device or params[0].device
+        layer_numel = sum(p.numel() for p in params)
+        state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
+        device = params[0].device
+        need = 2 * layer_numel * torch.empty(0, dtype=state_type).element_size()
+        if self.moments_device is not None and (self.moments_hbm_bytes is None or
+                                                self.moments_hbm_used + need <= self.moments_hbm_bytes):
+            device = self.moments_device
         if self.offloader is not None and device.type != 'cpu':
             # as in the reference, the file offload moves host-resident moments
             raise RuntimeError("nvme_offload_fraction > 0 needs host-resident params and state")
@@ -385,8 +401,6 @@ class LayerAdam:
             **self.defaults,
         }
         self.param_groups.append(param_group)
-        layer_numel = sum(p.numel() for p in params)
-        state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
         # host moments are page-locked on request: the copy engines then read and
         # write them directly, without the staging copies that pageable arrays
         # take (not with the file offload, which releases and re-allocates them)
@@ -395,6 +409,8 @@ class LayerAdam:
         self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device, pin_memory=pin)
         self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device,
                                                       pin_memory=pin)
+        if device == self.moments_device:
+            self.moments_hbm_used += need
         offset = 0
         for p in params:
             size = p.numel()

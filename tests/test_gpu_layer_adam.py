@@ -604,6 +604,38 @@ def test_moments_in_hbm_in_the_runtime_protocol(pinned, hip_device):
     check()
 
 
+def test_moments_hbm_budget_splits_layers(hip_device):
+    """LayerAdam(moments_device=..., moments_hbm_bytes=B): layers get HBM
+    moments while B allows, later ones keep host moments; every layer steps
+    bit-exact with the oracle whatever its placement (host master, host grads)."""
+    sizes = [5000, 3000, 4000, 7]
+    budget = 2 * 4 * (5000 + 3000)           # exactly the first two layers' m and v
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, moments_device=hip_device, moments_hbm_bytes=budget)
+    rng = np.random.default_rng(70)
+    masters, host = [], []
+    for i, k in enumerate(sizes):
+        p0 = rng.normal(0, 0.02, k).astype(np.float32)
+        t = torch.from_numpy(p0.copy())
+        masters.append(t)
+        host.append([p0.copy(), np.zeros(k, np.float32), np.zeros(k, np.float32)])
+        adam.add_layer_params(i, [torch.nn.Parameter(t)])
+    assert [adam.exp_avg_flat[i].is_cuda for i in range(4)] == [True, True, False, False]
+    assert adam.moments_hbm_used == budget
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for _ in range(2):
+        for i in reversed(range(4)):                 # sliding order
+            g = torch.from_numpy(rng.normal(0, 1e-3, sizes[i]).astype(np.float32)).bfloat16()
+            group = adam.begin_chunk_step(i)
+            adam.step_chunk(masters[i], g, adam.exp_avg_flat[i], adam.exp_avg_sq_flat[i], group)
+            adam.end_chunk_step(i)
+            orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, *host[i][:1], H.to_np_bits(g, "bf16"),
+                       *host[i][1:], g16="bf16")
+    for i in range(4):
+        assert np.array_equal(masters[i].numpy().view(np.uint32), host[i][0].view(np.uint32)), i
+        assert np.array_equal(H.to_np_bits(adam.exp_avg_flat[i], "f32"), host[i][1].view(np.uint32)), i
+        assert np.array_equal(H.to_np_bits(adam.exp_avg_sq_flat[i], "f32"), host[i][2].view(np.uint32)), i
+
+
 @pytest.mark.parametrize("triple", [("bf16", "bf16", "bf16"), ("f16", "f32", "f32"), ("f16", "f16", "f16")])
 def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
     """The streaming pipeline on the reference's other dtype triples: 16-bit

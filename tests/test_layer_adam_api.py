@@ -83,6 +83,10 @@ def test_moments_device_is_checked_at_construction(tmp_path):
     with pytest.raises(ValueError, match="exclude each other"):
         LayerAdam(moments_device="cuda:0", nvme_offload_fraction=0.5, offload_dir=str(tmp_path))
     assert LayerAdam(moments_device="cuda:0").moments_device == torch.device("cuda", 0)
+    with pytest.raises(ValueError, match="moments_hbm_bytes"):
+        LayerAdam(moments_hbm_bytes=1 << 30)
+    with pytest.raises(ValueError, match="moments_hbm_bytes"):
+        LayerAdam(moments_device="cuda:0", moments_hbm_bytes=-1)
 
 
 def test_argument_checks_precede_dispatch():
