@@ -377,6 +377,42 @@ def test_c2_llama8b_layer_full_size(hip_device):
     _full_size_step(n, hip_device, warm_steps=5, wd=0.01, seed=20)
 
 
+@pytest.mark.parametrize("triple,mode", [(("f32", "f32", "f32"), "adamw"), (("bf16", "bf16", "bf16"), "adamw"),
+                                         (("f16", "f16", "f32"), "l2"), (("bf16", "f32", "f32"), "adamw")])
+def test_c2_size_other_triples(triple, mode, hip_device):
+    """The reference's other registered triples (cpu_adam_impl.cpp:181-189) at the
+    C2 shape (218,112,000 elements, no tail), two steps with a clip coefficient
+    and the bf16 copy: every bit equals the oracle's."""
+    pk, gk, sk = triple
+    n = sum(llama8b_layer_sizes())
+    log(f"C2-size {triple} {mode}")
+    wd, adamw = (0.01, True) if mode == "adamw" else (0.01, False)
+    p_d = _dev_normal(n, 0.02, 60, hip_device).to(H.TD[pk])
+    m_d = torch.zeros(n, dtype=H.TD[sk], device=hip_device)
+    v_d = torch.zeros(n, dtype=H.TD[sk], device=hip_device)
+    out = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    p_h, m_h, v_h = H.to_np_bits(p_d, pk), H.to_np_bits(m_d, sk), H.to_np_bits(v_d, sk)
+    o_h = np.zeros(n, np.uint16)
+    coef = torch.tensor([0.75], device=hip_device)
+    hip = H.HipAdam(1e-5, (0.9, 0.999), 1e-8, wd, adamw)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, wd, adamw)
+    for st in (1, 2):
+        g = _dev_normal(n, 1e-3, 60 + st, hip_device).to(H.TD[gk])
+        hip.update(st, 1e-5, 0.9, 0.999, 1e-8, wd, True, p_d, g, m_d, v_d, out=out, coef=coef)
+        # the bf16 copy is RNE of the fp32 result, before any rounding to 16-bit params
+        orc.update(st, 1e-5, 0.9, 0.999, 1e-8, wd, True, _view(p_h, pk), _view(H.to_np_bits(g, gk), gk),
+                   _view(m_h, sk), _view(v_h, sk), p16=KIND16[pk], g16=KIND16[gk], s16=KIND16[sk],
+                   clip_coef=0.75, p_bf16_out=o_h)
+        del g
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p_d, pk), p_h)
+    assert np.array_equal(H.to_np_bits(m_d, sk), m_h)
+    assert np.array_equal(H.to_np_bits(v_d, sk), v_h)
+    assert np.array_equal(H.to_np_bits(out, "bf16"), o_h)
+    del p_d, m_d, v_d, out
+    torch.cuda.empty_cache()
+
+
 def test_c2_llama8b_layer_in_reference_chunks(hip_device):
     """The runtime's chunking: 32 Mi-element step_chunk calls (transformer_layer.py:26-27)."""
     n = sum(llama8b_layer_sizes())
