@@ -927,6 +927,64 @@ def test_c5_streamed_full_size_matches_resident(hip_device):
     torch.cuda.empty_cache()
 
 
+def test_streamed_call_beyond_2_pow_32_elements(hip_device):
+    """One step_chunk over n = 2^32 + 2^20 + 13 elements with the master in
+    pageable host memory (17 GB, staged through the page-locked twins) and the
+    moments, grads and bf16 copy in HBM: 257 pipeline chunks whose element and
+    byte offsets pass 2^32.  Same bits as the step on HBM-resident copies, and
+    windows at the start, across elements 2^31 and 2^32 and at the end (the
+    scalar tail) equal the oracle's."""
+    from slideformer_amd.layer_adam import HostStreamer
+
+    n = (1 << 32) + (1 << 20) + 13
+    print(f"streamed n={n}", flush=True)
+    gen = torch.Generator(device=hip_device)
+    gen.manual_seed(52)
+    p_d = torch.randn(n, generator=gen, device=hip_device) * 0.02
+    m_d = torch.randn(n, generator=gen, device=hip_device) * 1e-4
+    v_d = torch.rand(n, generator=gen, device=hip_device) * 1e-8
+    g = (torch.randn(n, generator=gen, device=hip_device) * 1e-3).bfloat16()
+    windows = [(0, 4096), ((1 << 31) - 2048, (1 << 31) + 2048), ((1 << 32) - 2048, (1 << 32) + 2048),
+               (n - 4096 - 13, n)]
+    init = [[t[lo:hi].cpu().numpy().copy() for t in (p_d, m_d, v_d)] for lo, hi in windows]
+    p_h = torch.empty(n, dtype=torch.float32)                    # pageable, as the runtime allocates it
+    piece = 256 * 1024 * 1024
+    for lo in range(0, n, piece):
+        p_h[lo:lo + piece].copy_(p_d[lo:lo + piece])
+    m_s, v_s = m_d.clone(), v_d.clone()
+    torch.cuda.synchronize()
+    print("host master ready", flush=True)
+
+    resident = LayerAdam(lr=1e-5, weight_decay=0.01)
+    out_d = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    resident.step_chunk(p_d, g, m_d, v_d, dict(resident.defaults, step=1), bf16_out=out_d)
+    streamed = LayerAdam(lr=1e-5, weight_decay=0.01)
+    streamed._streamers[hip_device] = HostStreamer(hip_device)
+    out_s = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    streamed.step_chunk(p_h, g, m_s, v_s, dict(streamed.defaults, step=1), bf16_out=out_s)
+    st = streamed.last_stream_stats
+    assert st.chunks == -(-n // (16 * 1024 * 1024)) == 257
+    assert st.h2d_bytes == st.d2h_bytes == 4 * n and st.staged_bytes == 8 * n
+    print(f"streamed step {st.wall_ms:.1f} ms; comparing", flush=True)
+    torch.cuda.synchronize()
+    for lo in range(0, n, piece):
+        assert torch.equal(p_h[lo:lo + piece].to(hip_device).view(torch.int32),
+                           p_d[lo:lo + piece].view(torch.int32)), lo
+    assert torch.equal(m_s.view(torch.int32), m_d.view(torch.int32))
+    assert torch.equal(v_s.view(torch.int32), v_d.view(torch.int32))
+    assert torch.equal(out_s.view(torch.int16), out_d.view(torch.int16))
+    for (lo, hi), (p0, m0, v0) in zip(windows, init):
+        orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+        orc.update(1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p0, H.to_np_bits(g[lo:hi], "bf16"), m0, v0, g16="bf16")
+        assert (hi - lo) % 16 == (n % 16 if hi == n else 0)
+        assert np.array_equal(p_h[lo:hi].numpy().view(np.uint32), p0.view(np.uint32)), lo
+        assert np.array_equal(H.to_np_bits(m_s[lo:hi], "f32"), m0.view(np.uint32)), lo
+        assert np.array_equal(H.to_np_bits(v_s[lo:hi], "f32"), v0.view(np.uint32)), lo
+        assert np.array_equal(H.to_np_bits(out_s[lo:hi], "bf16"), O.f32_to_bf16(p0)), lo
+    del p_h, p_d, m_d, v_d, m_s, v_s, g, out_d, out_s, streamed, resident
+    torch.cuda.empty_cache()
+
+
 def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     """la_pipeline_step validates the dtype triple and device-pointer alignment
     up front: the host state is left untouched."""
