@@ -62,8 +62,9 @@ SUPPORTED_TRIPLES = frozenset({
 # Llama-3.1-8B layer: with page-locked state, 4-16 Mi-element chunks with 3-4
 # slots all run at 46-47.5 GB/s each way (the concurrent-duplex limit of the
 # host link); with pageable state staged by host threads, 16 Mi x 3 runs at
-# 59-60 ms per layer every time while 8 Mi x 4 alternates between 59 and
-# 80-90 ms.
+# 59-60 ms per layer every time, while with four slots a D2H hipMemcpyAsync
+# into a page-locked twin now and then blocks the calling thread for 6-7 ms
+# and the pipeline drains (8 Mi x 4 and 16 Mi x 4: 80-90 ms).
 HOST_STAGE_ELEMS = 16 * 1024 * 1024
 HOST_STAGE_SLOTS = 3
 
