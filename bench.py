@@ -292,6 +292,71 @@ def streamed(args):
     print(json.dumps(res), flush=True)
 
 
+def copy_ceiling(args):
+    """What plain copies of the update's bytes reach on this GPU, next to the
+    update kernel itself, all in one process: one launch moves the bytes of one
+    C2 update launch, 14 B/param read and 14 B/param written
+    (3,053,568,000 B each way).  Three kernels, each timed over --steps
+    launches with HIP events:
+      - torch's device-to-device copy_ (the HIP runtime's copy kernel);
+      - torch's elementwise mul by 1.0 (one read stream, one write stream);
+      - la_adamw_kernel on the C2 layer (four read and four write streams)."""
+    import torch
+
+    from slideformer_amd import LayerAdam
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = sum(LLAMA8B_LAYER)
+    each_way = 14 * n
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(args.steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
+
+    src = torch.ones(each_way // 4, device=dev)
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src))
+    t_mul = timed(lambda: torch.mul(src, 1.0, out=dst))
+    del src, dst
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20)
+    p = torch.randn(n, generator=gen, device=dev) * 0.02
+    m = torch.zeros(n, device=dev)
+    v = torch.zeros(n, device=dev)
+    g = (torch.randn(n, generator=gen, device=dev) * 1e-3).bfloat16()
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+    step = [0]
+
+    def update():
+        step[0] += 1
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=step[0]), bf16_out=out)
+
+    t_upd = timed(update)
+    gbs = lambda ms: round(2 * each_way / (ms * 1e-3) / 1e9, 1)
+    res = {
+        "metric": "HBM copy ceiling for the bytes of one C2 update launch, GB/s",
+        "bytes_read": each_way, "bytes_written": each_way, "steps": args.steps,
+        "torch_copy_d2d": {"ms": round(t_copy, 4), "gbs": gbs(t_copy)},
+        "torch_elementwise_mul": {"ms": round(t_mul, 4), "gbs": gbs(t_mul)},
+        "la_adamw_kernel": {"ms": round(t_upd, 4), "gbs": gbs(t_upd)},
+        "update_vs_best_copy": round(min(t_copy, t_mul) / t_upd, 4),
+        "peak_gbs": PEAK_HBM_GBS,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def llama8b_model_sizes():
     """Flat buffer sizes of the Llama-3.1-8B-shaped model in layer-index order:
     embed, 32 decoder layers, final norm + lm_head (8,030,261,248 params)."""
@@ -656,6 +721,8 @@ def main():
                     help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
     ap.add_argument("--slots", type=int, default=0,
                     help="with --streamed c3-layer|c5: pipeline slots (default: the config's)")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="time plain HBM copies of one C2 update's bytes beside the update kernel")
     ap.add_argument("--moments-in-hbm", action="store_true",
                     help="--streamed: m and v stay in HBM, only the fp32 master is streamed")
     ap.add_argument("--host-grads", action="store_true",
@@ -697,6 +764,9 @@ def main():
         return
     if args.step_api:
         step_api(args)
+        return
+    if args.copy_ceiling:
+        copy_ceiling(args)
         return
     if args.config != "c2":
         resident_stack(args)
