@@ -316,6 +316,96 @@ def test_runtime_chunk_protocol_with_update_thread(hip_device):
     assert np.array_equal(H.to_np_bits(cache_unit, "bf16"), O.f32_to_bf16(p_h))
 
 
+@pytest.mark.parametrize("moments_in_hbm,pinned", [(False, False), (True, False), (True, True)])
+def test_runtime_protocol_on_host_state_with_shared_grad_buffer(moments_in_hbm, pinned, hip_device):
+    """The runtime's host-side protocol end to end, with injected delays as in
+    the reference's own test (test_shared_data_parallel.py:69,82): layers in
+    sliding order share ONE page-locked grad buffer (transformer_layer.py:206,
+    the shared cpu_grad_tensor); a producer copies each layer's device grads
+    into it chunk by chunk, recording an event per chunk (:343-422), but
+    starts a layer only after the previous layer's update_finished (:348-351);
+    an update thread waits on each event and calls step_chunk on the host
+    master chunk, the shared grad chunk and the moments (:453-493), with
+    overlap_host_chunks=True, then end_chunk_step and update_finished.  Three
+    steps, bit-exact with the oracle; host moments or moments in HBM;
+    pageable or page-locked masters."""
+    import queue
+    import threading
+    import time
+
+    sizes, chunk = [20_000, 7, 13_003], 4096
+    rng = np.random.default_rng(41 + 2 * int(moments_in_hbm) + int(pinned))
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, overlap_host_chunks=True,
+                     moments_device=hip_device if moments_in_hbm else None)
+    from slideformer_amd.layer_adam import HostStreamer
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=2048, slots=3)
+    masters, host = [], []
+    for i, k in enumerate(sizes):
+        p0 = rng.normal(0, 0.02, k).astype(np.float32)
+        t = torch.from_numpy(p0.copy())
+        masters.append(t.pin_memory() if pinned else t)
+        host.append([p0.copy(), np.zeros(k, np.float32), np.zeros(k, np.float32)])
+        adam.add_layer_params(i, [torch.nn.Parameter(masters[i])])
+    shared_grad = torch.empty(max(sizes), dtype=torch.bfloat16, pin_memory=True)
+    producer = torch.cuda.Stream(device=hip_device)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    finished_prev = threading.Event()
+    finished_prev.set()
+    errors = []
+    for step in range(1, 4):
+        for i in reversed(range(len(sizes))):                      # sliding order
+            k = sizes[i]
+            g_dev = (torch.from_numpy(rng.normal(0, 1e-3, k).astype(np.float32))).bfloat16().to(hip_device)
+            g_bits = H.to_np_bits(g_dev, "bf16")
+            q: "queue.Queue" = queue.Queue()
+            finished = threading.Event()
+
+            def update_thread(i=i, q=q, finished=finished):
+                try:
+                    group = adam.begin_chunk_step(i)
+                    while True:
+                        item = q.get()
+                        if item is None:
+                            break
+                        cs, ce, ev = item
+                        ev.synchronize()
+                        adam.step_chunk(masters[i][cs:ce], shared_grad[cs:ce], adam.exp_avg_flat[i][cs:ce],
+                                        adam.exp_avg_sq_flat[i][cs:ce], group)
+                        time.sleep(float(rng.uniform(0, 0.002)))
+                    adam.end_chunk_step(i)
+                except Exception as exc:
+                    errors.append(exc)
+                finally:
+                    finished.set()
+
+            # the next layer's D2H into the shared buffer waits for the previous update
+            assert finished_prev.wait(timeout=60)
+            t = threading.Thread(target=update_thread)
+            t.start()
+            with torch.cuda.stream(producer):
+                for cs in range(0, k, chunk):
+                    ce = min(cs + chunk, k)
+                    shared_grad[cs:ce].copy_(g_dev[cs:ce], non_blocking=True)
+                    ev = torch.cuda.Event()
+                    ev.record(producer)
+                    q.put((cs, ce, ev))
+                    time.sleep(float(rng.uniform(0, 0.002)))
+            q.put(None)
+            t.join(timeout=60)
+            assert not t.is_alive()
+            assert not errors, errors
+            finished_prev = finished
+            for cs in range(0, k, chunk):
+                ce = min(cs + chunk, k)
+                orc.update(adam.param_groups[i]["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True,
+                           host[i][0][cs:ce], g_bits[cs:ce], host[i][1][cs:ce], host[i][2][cs:ce], g16="bf16")
+    torch.cuda.synchronize()
+    for i in range(len(sizes)):
+        assert np.array_equal(masters[i].numpy().view(np.uint32), host[i][0].view(np.uint32)), i
+        assert np.array_equal(H.to_np_bits(adam.exp_avg_flat[i], "f32"), host[i][1].view(np.uint32)), i
+        assert np.array_equal(H.to_np_bits(adam.exp_avg_sq_flat[i], "f32"), host[i][2].view(np.uint32)), i
+
+
 @pytest.mark.parametrize("fraction,prefetch", [(1.0, True), (0.3, False)])
 def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path):
     """Host state with the moments offloaded to files between layer steps
