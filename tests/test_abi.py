@@ -17,8 +17,13 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO, "include", "layer_adam.h")
 
 
+def _read(path, mode="r"):
+    with open(path, mode) as f:
+        return f.read()
+
+
 def declared_functions():
-    text = open(HEADER).read()
+    text = _read(HEADER)
     return sorted(set(re.findall(r"^\s*(?:int|uint64_t|const char\*)\s+(la_\w+)\s*\(", text, re.M)))
 
 
@@ -30,9 +35,9 @@ def test_library_exports_every_declared_symbol():
     L = _lib.load()
     for name in declared_functions():
         assert hasattr(L, name), name
-    version = int(re.search(r"#define LA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
     assert L.la_abi_version() == version == 5
-    header = open(HEADER).read()
+    header = _read(HEADER)
     for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
                  "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):
         value = int(re.search(rf"#define {name} \(?(-?\d+)u?\)?", header).group(1))
@@ -41,7 +46,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_is_gfx950_code_object():
     # the fat binary embeds an amdgcn code object for gfx950 only
-    blob = open(_lib.LIB_PATH, "rb").read()
+    blob = _read(_lib.LIB_PATH, "rb")
     assert b"gfx950" in blob
     for other in (b"gfx942", b"gfx90a", b"gfx1100"):
         assert other not in blob
@@ -204,7 +209,7 @@ def test_segment_layout_is_six_words():
     S = _lib.LaSegment
     assert ctypes.sizeof(S) == 48
     assert [getattr(S, f).offset for f in ("p", "g", "m", "v", "p_bf16_out", "n")] == [0, 8, 16, 24, 32, 40]
-    header = open(HEADER).read()
+    header = _read(HEADER)
     body = re.search(r"typedef struct \{([^}]*)\} la_segment_t;", header).group(1)
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
     names = re.findall(r"(\w+);", body)
