@@ -357,6 +357,52 @@ def copy_ceiling(args):
     print(json.dumps(res), flush=True)
 
 
+def triples(args):
+    """The update kernel on every dtype triple the reference registers
+    (cpu_adam_impl.cpp:181-189), at the C2 shape (218,112,000 elements), with
+    the bf16 copy: --steps launches each, HIP events.  Algorithmic bytes per
+    element = read p + g + m + v, write p + m + v + the 2-byte copy."""
+    import torch
+
+    from slideformer_amd import LayerAdam, SUPPORTED_TRIPLES
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = sum(LLAMA8B_LAYER)
+    stream = torch.cuda.current_stream(dev)
+    names = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+    rows = []
+    for pd, gd, sd in SUPPORTED_TRIPLES:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(20)
+        p = (torch.randn(n, generator=gen, device=dev) * 0.02).to(pd)
+        g = (torch.randn(n, generator=gen, device=dev) * 1e-3).to(gd)
+        m = torch.zeros(n, dtype=sd, device=dev)
+        v = torch.zeros(n, dtype=sd, device=dev)
+        out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+        for t in range(1, 4):
+            adam.step_chunk(p, g, m, v, dict(adam.defaults, step=t), bf16_out=out)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for t in range(4, 4 + args.steps):
+            adam.step_chunk(p, g, m, v, dict(adam.defaults, step=t), bf16_out=out)
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / args.steps
+        per = 2 * p.element_size() + g.element_size() + 4 * m.element_size() + 2
+        rows.append({"triple": [names[pd], names[gd], names[sd]], "bytes_per_param": per, "ms": round(ms, 4),
+                     "gparams_s": round(n / (ms * 1e-3) / 1e9, 1),
+                     "gbs": round(per * n / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(per * n / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+        log(f"{rows[-1]}")
+        del p, g, m, v, out
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "update kernel per dtype triple, C2 shape", "params": n, "steps": args.steps,
+                      "results": rows}), flush=True)
+
+
 def llama8b_model_sizes():
     """Flat buffer sizes of the Llama-3.1-8B-shaped model in layer-index order:
     embed, 32 decoder layers, final norm + lm_head (8,030,261,248 params)."""
@@ -721,6 +767,8 @@ def main():
                     help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
     ap.add_argument("--slots", type=int, default=0,
                     help="with --streamed c3-layer|c5: pipeline slots (default: the config's)")
+    ap.add_argument("--triples", action="store_true",
+                    help="time the update kernel on every registered dtype triple at the C2 shape")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain HBM copies of one C2 update's bytes beside the update kernel")
     ap.add_argument("--moments-in-hbm", action="store_true",
@@ -767,6 +815,9 @@ def main():
         return
     if args.copy_ceiling:
         copy_ceiling(args)
+        return
+    if args.triples:
+        triples(args)
         return
     if args.config != "c2":
         resident_stack(args)

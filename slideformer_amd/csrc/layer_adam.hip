@@ -34,6 +34,7 @@
 #include <cstring>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -83,13 +84,23 @@
 #define LA_SETPRIO 1
 #endif
 // Dynamic LDS reserved per update workgroup, unused by the kernel: it caps the
-// workgroups (= waves) resident per CU at 160 KiB / LA_UPDATE_LDS_BYTES, 16 for
+// workgroups (= waves) resident per CU at 160 KiB / (reserved bytes), 16 for
 // 10 KiB.  Fewer streams in flight at once keep the HBM row buffers busier.
-// Measured on MI355X, C2 layer, same box: uncapped (32 waves per CU, the
-// register limit) 0.947 ms; 26 per CU 0.942; 20 0.918; 17-16 0.9135; 15-14
-// 0.917; 13-12 0.950-0.986; 8 1.18 ms.  Wave priority and the write-through
-// stores still add 1-3 % on top of the cap.
-#ifndef LA_UPDATE_LDS_BYTES
+// Measured on MI355X, C2 layer, (f32, bf16, f32), same box: uncapped (32
+// waves per CU, the register limit) 0.947 ms; 26 per CU 0.942; 20 0.918;
+// 17-16 0.9135; 15-14 0.917; 13-12 0.950-0.986; 8 1.18 ms.  Wave priority and
+// the write-through stores still add 1-3 % on top of the cap.
+// The triples with 16-bit moments move fewer bytes per element for the same
+// arithmetic and conversions, and need the waves to hide it: at the C2 shape,
+// (bf16, bf16, bf16) 0.865 ms capped at 16 waves against 0.581 uncapped,
+// (f16, f16, f16) 1.070 against 0.715, (f16, f16, f32) 0.964 against 0.834;
+// (bf16, bf16, f32) is best at 20 waves (8 KiB: 0.817 against 0.848 at 16 and
+// 0.853 uncapped).  The other triples keep 16.  LA_UPDATE_LDS_BYTES, when
+// defined, overrides the table for every triple.
+#ifdef LA_UPDATE_LDS_BYTES
+#define LA_UPDATE_LDS_OVERRIDE 1
+#else
+#define LA_UPDATE_LDS_OVERRIDE 0
 #define LA_UPDATE_LDS_BYTES 10240
 #endif
 static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
@@ -682,6 +693,17 @@ int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes, 
     return hip_rc(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds_bytes, stream));
 }
 
+// LDS reserved per update workgroup for one (param, grad, state) triple (see
+// LA_UPDATE_LDS_BYTES); 0 = no cap below the register limit.
+template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_bytes()
+{
+    if (LA_UPDATE_LDS_OVERRIDE) return LA_UPDATE_LDS_BYTES;
+    if (std::is_same<TS, bf16_t>::value || std::is_same<TS, f16_t>::value) return 0;          // 16-bit moments
+    if (std::is_same<TP, f16_t>::value && std::is_same<TG, f16_t>::value) return 0;           // (f16, f16, f32)
+    if (std::is_same<TP, bf16_t>::value && std::is_same<TG, bf16_t>::value) return 8192;      // (bf16, bf16, f32)
+    return LA_UPDATE_LDS_BYTES;
+}
+
 template <typename TP, typename TG, typename TS> struct StepLauncher {
     static int run(const StepArgs& a, hipStream_t stream)
     {
@@ -690,7 +712,7 @@ template <typename TP, typename TG, typename TS> struct StepLauncher {
         const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
         const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
         return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
-                      LA_UPDATE_LDS_BYTES, stream, a);
+                      update_lds_bytes<TP, TG, TS>(), stream, a);
     }
 };
 
@@ -699,7 +721,7 @@ template <typename TP, typename TG, typename TS> struct MultiLauncher {
     static int run(const MultiArgs& a, uint64_t waves, hipStream_t stream)
     {
         return launch(la_adamw_multi_kernel<TP, TG, TS>, dim3(static_cast<uint32_t>(waves * 64 / LA_BLOCK)),
-                      dim3(LA_BLOCK), LA_UPDATE_LDS_BYTES, stream, a);
+                      dim3(LA_BLOCK), update_lds_bytes<TP, TG, TS>(), stream, a);
     }
 };
 
