@@ -659,3 +659,38 @@ def test_plain_c_program_runs_the_step(tmp_path):
     assert np.array_equal(gm.view(np.uint32), m.view(np.uint32))
     assert np.array_equal(gv.view(np.uint32), v.view(np.uint32))
     assert np.array_equal(gout, O.f32_to_bf16(p))
+
+
+def test_bf16_copy_rounding_of_every_fp32_bit_pattern(hip_device):
+    """The bf16 compute copy, brute force over all 2^32 fp32 bit patterns: with
+    lr = 0, zero grads and zero moments the update leaves every master value
+    as it is (p + 0 * -0), so the copy the kernel writes is the rounding of an
+    arbitrary fp32 input.  It must equal the reference's bf16 store,
+    (u + 0x7FFF + ((u >> 16) & 1)) >> 16 with NaN -> 0x7FC0 (simd.h:56-86),
+    for every input; computed on the device in 16 launches of 2^28."""
+    chunk = 1 << 28
+    hip = H.HipAdam(0.0, (0.9, 0.999), 1e-8, 0.0, True)
+    g = torch.zeros(chunk, dtype=torch.bfloat16, device=hip_device)
+    m = torch.zeros(chunk, device=hip_device)
+    v = torch.zeros(chunk, device=hip_device)
+    out = torch.empty(chunk, dtype=torch.bfloat16, device=hip_device)
+    for c in range(16):
+        log(f"bf16 rounding, patterns [{c * chunk:#x}, {(c + 1) * chunk:#x})")
+        bits = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int64, device=hip_device)
+        p = bits.to(torch.int32).view(torch.float32)       # wraps to the int32 bit pattern
+        del bits
+        m.zero_()
+        v.zero_()
+        hip.update(c + 1, 0.0, 0.9, 0.999, 1e-8, 0.0, True, p, g, m, v, out=out)
+        u = p.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+        want = torch.where((u & 0x7FFFFFFF) > 0x7F800000, torch.full_like(want, 0x7FC0), want)
+        got = out.view(torch.int16).to(torch.int64) & 0xFFFF
+        bad = int((got != want).sum().item())
+        assert bad == 0, (c, bad)
+        # the master itself is unchanged (NaN stays NaN)
+        orig = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int64, device=hip_device)
+        same = (u == (orig & 0xFFFFFFFF)) | ((u & 0x7FFFFFFF) > 0x7F800000)
+        assert bool(same.all()), c
+        del p, u, want, got, orig, same
+    torch.cuda.empty_cache()
