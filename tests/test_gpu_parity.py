@@ -694,3 +694,40 @@ def test_bf16_copy_rounding_of_every_fp32_bit_pattern(hip_device):
         assert bool(same.all()), c
         del p, u, want, got, orig, same
     torch.cuda.empty_cache()
+
+
+def test_fp16_store_rounding_of_every_fp32_bit_pattern(hip_device):
+    """The fp16 store (hardware conversion behind an opaque value), brute force
+    over all 2^32 fp32 bit patterns via the (f16, f32, f32) triple: with lr 1,
+    betas (0, 1), eps 0, no decay and no bias correction, p = 0, m = 0, v = 1,
+    the update computes m = g, v = 1, d = 1, u = g and p = fma(u, -1, 0) = -g
+    exactly, then stores p as fp16.  That must equal the CPU's IEEE
+    round-to-nearest-even of the same fp32 value (0 + -g; torch's CPU
+    conversion, the x86 F16C instruction), NaN as a class.
+    Patterns with |g| >= 2^63 are left out: there g*g overflows and v turns
+    NaN (every fp16 of them would be +-inf anyway)."""
+    chunk = 1 << 28
+    hip = H.HipAdam(1.0, (0.0, 1.0), 0.0, 0.0, True)
+    p = torch.zeros(chunk, dtype=torch.float16, device=hip_device)
+    m = torch.zeros(chunk, device=hip_device)
+    v = torch.ones(chunk, device=hip_device)
+    checked = 0
+    for c in range(16):
+        log(f"fp16 rounding, patterns [{c * chunk:#x}, {(c + 1) * chunk:#x})")
+        g = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int64, device=hip_device).to(
+            torch.int32).view(torch.float32)
+        p.zero_()
+        m.zero_()
+        v.fill_(1.0)
+        hip.update(c + 1, 1.0, 0.0, 1.0, 0.0, 0.0, False, p, g, m, v)
+        g_h = g.cpu()
+        got = p.cpu()
+        want = (torch.zeros((), dtype=torch.float32) + (-g_h)).to(torch.float16)
+        skip = g_h.abs() >= 2.0 ** 63                       # NaN compares false: kept
+        nan = want.isnan()
+        assert bool(((got.isnan() == nan) | skip).all()), c
+        assert bool(((got.view(torch.int16) == want.view(torch.int16)) | skip | nan).all()), c
+        checked += g_h.numel() - int(skip.sum())
+        del g, g_h, got, want, skip, nan
+    assert checked > (1 << 32) - (1 << 31)
+    torch.cuda.empty_cache()
