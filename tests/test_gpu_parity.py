@@ -731,3 +731,46 @@ def test_fp16_store_rounding_of_every_fp32_bit_pattern(hip_device):
         del g, g_h, got, want, skip, nan
     assert checked > (1 << 32) - (1 << 31)
     torch.cuda.empty_cache()
+
+
+def test_sqrt_and_divide_over_fp32_bit_patterns(hip_device):
+    """The kernel's correctly rounded sqrt and division over fp32 bit patterns
+    of v via the (f32, f32, f32) triple: with lr 1, betas (0, 1), eps 0, no
+    decay, no bias correction, g = 1, m = 0, p = 0 the body computes m = 1,
+    v' = v * 1 + 1 * 0, d = sqrt(v') * 1 + 0, u = m / d and p = u * -1 + 0
+    (cpu_adam.h:159-192).  Patterns, both signs: every one with exponent field
+    0 or 1 (denormals and the smallest normals), every one with exponent field
+    0xFE or 0xFF (the largest normals, Inf, NaN), and every 61st of the rest.
+    The CPU computes the same sequence in float64 and rounds to float32 once
+    per operation; float64 carries 53 >= 2 x 24 + 2 bits, so that equals the
+    correctly rounded float32 sqrt and division.  (torch's own CPU float32
+    sqrt is not correctly rounded: it differs from numpy's float32 sqrt on
+    about 0.6 % of random inputs, so it cannot serve here.)  Every bit of p
+    must match, NaN as a class."""
+    parts = []
+    for sign in (0, 1 << 31):
+        parts.append(torch.arange(0, 1 << 24, dtype=torch.int64) + sign)                 # exponent 0, 1
+        parts.append(torch.arange(0xFE << 23, 1 << 31, dtype=torch.int64) + sign)         # exponent 0xFE, 0xFF
+    parts.append(torch.arange(1 << 24, 1 << 32, 61, dtype=torch.int64))                  # the rest, both signs
+    pats = torch.cat(parts)
+    n = pats.numel()
+    log(f"sqrt/divide over {n} patterns")
+    v_h = pats.to(torch.int32).view(torch.float32)
+    del parts, pats
+    hip = H.HipAdam(1.0, (0.0, 1.0), 0.0, 0.0, True)
+    v = v_h.to(hip_device)
+    p = torch.zeros(n, device=hip_device)
+    m = torch.zeros(n, device=hip_device)
+    g = torch.ones(n, device=hip_device)
+    hip.update(1, 1.0, 0.0, 1.0, 0.0, 0.0, False, p, g, m, v)
+    got = p.cpu()
+    log("GPU done; CPU reference")
+    v1 = (v_h.to(torch.float64) * 1.0 + 0.0).to(torch.float32)
+    d = (torch.sqrt(v1.to(torch.float64)).to(torch.float32).to(torch.float64) * 1.0 + 0.0).to(torch.float32)
+    u = (1.0 / d.to(torch.float64)).to(torch.float32)
+    want = (0.0 + -u.to(torch.float64)).to(torch.float32)
+    nan = want.isnan()
+    assert bool((got.isnan() == nan).all())
+    assert bool(((got.view(torch.int32) == want.view(torch.int32)) | nan).all())
+    del v, p, m, g, got, v_h, v1, d, u, want, nan
+    torch.cuda.empty_cache()
