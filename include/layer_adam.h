@@ -186,7 +186,9 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  * la_pipeline_step: one reference adam_update over n elements (p, m, v, g
  *   and the nullable bf16 copy `out` placed as `on_host` says; host arrays
  *   page-locked for full speed).  Work queued on `after` before the call
- *   runs first; work queued on `after` later sees the result.
+ *   runs first; work queued on `after` later sees the result.  A call that
+ *   copies pageable arrays through the host staging first waits on the host
+ *   for that earlier work, since its threads read host memory directly.
  *   synchronize != 0 (or stats != NULL) waits for completion of this call
  *   and of every earlier one.  With synchronize == 0 the call returns once
  *   its work is queued, and work queued on `after` later is not ordered
