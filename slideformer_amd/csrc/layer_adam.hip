@@ -691,6 +691,16 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_b
     return LA_UPDATE_LDS_BYTES;
 }
 
+// The multi kernel's waves first look up their segment and its arguments, a
+// latency that more resident waves hide better: at most 8 KiB (20 waves per
+// CU).  Measured on MI355X, a GPT-2 block's twelve tensors in one launch:
+// (f32, bf16, f32) 33.5 us at 16 waves, 32.5 at 20, 31.9 uncapped;
+// (f32, f32, f32) 32.3, 31.9, 34.1.
+template <typename TP, typename TG, typename TS> constexpr uint32_t multi_lds_bytes()
+{
+    return update_lds_bytes<TP, TG, TS>() < 8192u ? update_lds_bytes<TP, TG, TS>() : 8192u;
+}
+
 template <typename TP, typename TG, typename TS> struct StepLauncher {
     static int run(const StepArgs& a, hipStream_t stream)
     {
@@ -708,7 +718,7 @@ template <typename TP, typename TG, typename TS> struct MultiLauncher {
     static int run(const MultiArgs& a, uint64_t waves, hipStream_t stream)
     {
         return launch(la_adamw_multi_kernel<TP, TG, TS>, dim3(static_cast<uint32_t>(waves * 64 / LA_BLOCK)),
-                      dim3(LA_BLOCK), update_lds_bytes<TP, TG, TS>(), stream, a);
+                      dim3(LA_BLOCK), multi_lds_bytes<TP, TG, TS>(), stream, a);
     }
 };
 
