@@ -695,10 +695,15 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_b
 // latency that more resident waves hide better: at most 8 KiB (20 waves per
 // CU).  Measured on MI355X, a GPT-2 block's twelve tensors in one launch:
 // (f32, bf16, f32) 33.5 us at 16 waves, 32.5 at 20, 31.9 uncapped;
-// (f32, f32, f32) 32.3, 31.9, 34.1.
+// (f32, f32, f32) 32.3, 31.9, 34.1.  LA_MULTI_LDS_BYTES, when defined,
+// overrides it for every triple.
 template <typename TP, typename TG, typename TS> constexpr uint32_t multi_lds_bytes()
 {
+#ifdef LA_MULTI_LDS_BYTES
+    return LA_MULTI_LDS_BYTES;
+#else
     return update_lds_bytes<TP, TG, TS>() < 8192u ? update_lds_bytes<TP, TG, TS>() : 8192u;
+#endif
 }
 
 template <typename TP, typename TG, typename TS> struct StepLauncher {
