@@ -774,3 +774,32 @@ def test_sqrt_and_divide_over_fp32_bit_patterns(hip_device):
     assert bool(((got.view(torch.int32) == want.view(torch.int32)) | nan).all())
     del v, p, m, g, got, v_h, v1, d, u, want, nan
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("pk,gk", [("f16", "f16"), ("bf16", "bf16")])
+def test_16bit_params_of_every_pattern_round_trip(pk, gk, hip_device):
+    """Every one of the 65,536 fp16 / bf16 patterns as a 16-bit master, with
+    lr 0, zero grads and zero fp32 moments (the (f16, f16, f32) and
+    (bf16, bf16, f32) triples): the update leaves the value as it is, so the
+    stored master equals its input bit for bit (NaN as a class), and the bf16
+    copy is the bf16 rounding of the exactly widened input (numpy's float16
+    widening, the reference's bf16 formula in the oracle)."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    p = H.to_dev_bits(bits, pk, hip_device)
+    g = torch.zeros(bits.size, dtype=H.TD[gk], device=hip_device)
+    m = torch.zeros(bits.size, device=hip_device)
+    v = torch.zeros(bits.size, device=hip_device)
+    out = torch.empty(bits.size, dtype=torch.bfloat16, device=hip_device)
+    hip = H.HipAdam(0.0, (0.9, 0.999), 1e-8, 0.0, True)
+    hip.update(1, 0.0, 0.9, 0.999, 1e-8, 0.0, True, p, g, m, v, out=out)
+    torch.cuda.synchronize()
+    got = H.to_np_bits(p, pk)
+    wide = bits.view(np.float16).astype(np.float32) if pk == "f16" else O.bf16_to_f32(bits)
+    nan = np.isnan(wide)
+    assert np.array_equal(got[~nan], bits[~nan])
+    got_f = got.view(np.float16).astype(np.float32) if pk == "f16" else O.bf16_to_f32(got)
+    assert np.isnan(got_f[nan]).all()
+    o = H.to_np_bits(out, "bf16")
+    want = O.f32_to_bf16(wide)
+    assert np.array_equal(o[~nan], want[~nan])
+    assert (o[nan] == 0x7FC0).all()
