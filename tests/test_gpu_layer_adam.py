@@ -727,10 +727,12 @@ def test_moments_hbm_budget_splits_layers(hip_device):
 
 
 @pytest.mark.parametrize("triple", [("bf16", "bf16", "bf16"), ("f16", "f32", "f32"), ("f16", "f16", "f16")])
-def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
+@pytest.mark.parametrize("moments", ["host", "hbm"])
+def test_pipeline_other_triples_staged_and_overlapped(triple, moments, hip_device):
     """The streaming pipeline on the reference's other dtype triples: 16-bit
     params and states, host grads and a host bf16 copy, all pageable (staged),
-    overlapped calls of 3000 elements through 1024-element chunks in 2 slots.
+    overlapped calls of 3000 elements through 1024-element chunks in 2 slots;
+    the moments on the host or in HBM (mixed element sizes per placement).
     Bit-exact with the oracle."""
     from slideformer_amd.layer_adam import HostStreamer
     pk, gk, sk = triple
@@ -741,6 +743,8 @@ def test_pipeline_other_triples_staged_and_overlapped(triple, hip_device):
     p = torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).to(td[pk])
     m = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).to(td[sk])
     v = torch.from_numpy(np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)).to(td[sk])
+    if moments == "hbm":
+        m, v = m.to(hip_device), v.to(hip_device)
     out = torch.empty(n, dtype=torch.bfloat16)
     bits = lambda t, k: H.to_np_bits(t, k)
     hp, hm, hv = bits(p, pk), bits(m, sk), bits(v, sk)
