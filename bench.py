@@ -792,7 +792,9 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
-              "(the LayerAdam step is elementwise and would shard by contiguous slices; see DESIGN.md)",
+              "(the LayerAdam step is elementwise: it would shard by contiguous 1/W slices of each flat "
+              "layer buffer, with a reduce-scatter of the grads before it and an all-gather of the "
+              "bf16 copy after it)",
               file=sys.stderr)
         sys.exit(2)
 
