@@ -449,6 +449,13 @@ try {
             if (rc != LA_OK) return drain_streams(pl, rc);
         }
         if (staged) {
+            // The twin may still be the source of the previous chunk of slot s:
+            // its H2D waits behind that slot's earlier copy-back and can be
+            // queued well after this point.  When copy-outs were owed, settle()
+            // already waited for the copy-back, which follows the H2D; when only
+            // inputs were staged (pageable grads beside pinned or device state),
+            // nothing else holds the host back from overwriting the twin.
+            if (pl->slot_used[s]) LA_STEP_TRY(hipEventSynchronize(pl->ev_h2d[s]));
             if (st_p) add_pieces(pieces, hs + L.p, pp + off * pb, k * pb);
             if (st_m) add_pieces(pieces, hs + L.m, mp + off * sb, k * sb);
             if (st_v) add_pieces(pieces, hs + L.v, vp + off * sb, k * sb);

@@ -633,6 +633,40 @@ def test_pipeline_mixed_placements_match_oracle(name, pinned, hip_device):
     assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(ph))
 
 
+def test_staged_grads_only_wait_for_the_twins_copy_in(hip_device):
+    """Pageable grads are the only staged array: no copy-out is ever owed, so
+    before the host threads refill a slot's page-locked twin they must wait for
+    the H2D that still reads it (that H2D queues behind the slot's earlier
+    copy-back).  Many 256-element chunks over 2 slots with a single host thread
+    let the host run far ahead of the copy stream; every chunk's grads differ,
+    and the result must equal the oracle bit for bit."""
+    from slideformer_amd.layer_adam import HostStreamer
+    n, chunk = 400 * 256 + 7, 256
+    rng = np.random.default_rng(4242)
+    ph = rng.normal(0, 0.02, n).astype(np.float32)
+    mh = rng.normal(0, 1e-3, n).astype(np.float32)
+    vh = np.abs(rng.normal(0, 1e-6, n)).astype(np.float32)
+    p, m, v = (torch.from_numpy(a.copy()).to(hip_device) for a in (ph, mh, vh))
+    out = torch.empty(n, dtype=torch.bfloat16, device=hip_device)
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=chunk, slots=2, host_threads=1)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        print(f"grads-only staging, step {step}", flush=True)
+        g = torch.from_numpy(rng.normal(0, 1e-3, n).astype(np.float32)).bfloat16()
+        assert not g.is_pinned()
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=step), bf16_out=out)
+        st = adam.last_stream_stats
+        assert st.chunks == -(-n // chunk)
+        assert st.staged_bytes == 2 * n and st.h2d_bytes == 2 * n and st.d2h_bytes == 0
+        orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph, H.to_np_bits(g, "bf16"), mh, vh, g16="bf16")
+    torch.cuda.synchronize()
+    assert np.array_equal(H.to_np_bits(p, "f32"), ph.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(m, "f32"), mh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(v, "f32"), vh.view(np.uint32))
+    assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(ph))
+
+
 @pytest.mark.parametrize("pinned", [True, False])
 def test_moments_in_hbm_in_the_runtime_protocol(pinned, hip_device):
     """LayerAdam(moments_device=...) under the runtime's calls
