@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import Dict, List
+from typing import Dict, List, Set
 
 import torch
 
@@ -38,6 +38,9 @@ class DiskOffloader:
         self._nbytes: Dict[int, int] = {}
         self._pending_writes: List[torch.Tensor] = []
         self._pending_reads: List[torch.Tensor] = []
+        # keys with a native write not yet fenced by la_disk_sync_writes (a
+        # cancelled release leaves its write running)
+        self._writing: Set[int] = set()
 
     @staticmethod
     def _check_tensor(t: torch.Tensor):
@@ -55,9 +58,19 @@ class DiskOffloader:
         nbytes = tensor.numel() * tensor.element_size()
         if tensor.untyped_storage().nbytes() < nbytes:
             raise RuntimeError("async_write of a buffer whose storage was already released")
-        self._nbytes[id(tensor)] = nbytes
-        self._io_error(self.lib.la_disk_write_async(self.handle, id(tensor), tensor.data_ptr(), nbytes),
+        key = id(tensor)
+        if key in self._writing:
+            # An earlier write of this buffer is still running (async_read
+            # cancelled its release, and the buffer may have changed since).
+            # The pool's workers take pieces in parallel, so an old piece could
+            # land after the new one: fence the old write first.
+            rc = self.lib.la_disk_sync_writes(self.handle)
+            self._writing.clear()
+            self._io_error(rc, "la_disk_sync_writes")
+        self._nbytes[key] = nbytes
+        self._io_error(self.lib.la_disk_write_async(self.handle, key, tensor.data_ptr(), nbytes),
                        "la_disk_write_async")
+        self._writing.add(key)
         self._pending_writes.append(tensor)
 
     def async_read(self, tensor: torch.Tensor) -> None:
@@ -80,6 +93,7 @@ class DiskOffloader:
 
     def sync_write_events(self) -> None:
         rc = self.lib.la_disk_sync_writes(self.handle)
+        self._writing.clear()
         written, self._pending_writes = self._pending_writes, []
         self._io_error(rc, "la_disk_sync_writes")
         for t in written:

@@ -129,6 +129,53 @@ def test_disk_offloader_round_trip(tmp_path):
     assert list(tmp_path.glob("offload-*")) == []
 
 
+def test_disk_offloader_never_overlaps_two_writes_of_one_buffer(tmp_path):
+    """The reference's prefetch=False hooks (layer_adam.py:226-247) read a layer
+    back while its last write is unfenced, step it and write it again.  The
+    first write must be fenced before the second is queued (else an old piece
+    can land last); the bytes read back after a fenced release are the newest."""
+    from slideformer_amd.nvme import DiskOffloader
+    off = DiskOffloader(str(tmp_path), 4)
+    calls = []
+
+    class Recorder:
+        def __init__(self, lib):
+            self._lib = lib
+
+        def __getattr__(self, name):
+            fn = getattr(self._lib, name)
+
+            def wrapped(*args):
+                calls.append(name)
+                return fn(*args)
+            return wrapped
+
+    off.lib = Recorder(off.lib)
+    m = torch.randn(3 * (1 << 20))
+    off.async_write(m)          # _post_step: offload
+    off.async_read(m)           # next _pre_step: release cancelled, write still queued
+    m.mul_(0.5)                 # the step
+    off.async_write(m)          # _post_step again
+    assert calls == ["la_disk_write_async", "la_disk_sync_writes", "la_disk_write_async"]
+    newest = m.clone()
+    off.sync_write_events()
+    assert m.untyped_storage().nbytes() == 0
+    off.async_read(m)
+    off.sync_read_events()
+    assert torch.equal(m, newest)
+    # fenced writes need no extra fence
+    calls.clear()
+    off.async_write(m)
+    off.sync_write_events()
+    off.async_read(m)
+    off.sync_read_events()
+    off.async_write(m)
+    assert calls == ["la_disk_write_async", "la_disk_sync_writes", "la_disk_read_async", "la_disk_sync_reads",
+                     "la_disk_write_async"]
+    off.sync_write_events()
+    del off
+
+
 def test_disk_offloader_errors(tmp_path):
     from slideformer_amd.nvme import DiskOffloader
     not_a_dir = tmp_path / "plain_file"
