@@ -84,24 +84,27 @@
 #define LA_SETPRIO 1
 #endif
 // Dynamic LDS reserved per update workgroup, unused by the kernel: it caps the
-// workgroups (= waves) resident per CU at 160 KiB / (reserved bytes), 16 for
-// 10 KiB.  Fewer streams in flight at once keep the HBM row buffers busier.
-// Measured on MI355X, C2 layer, (f32, bf16, f32), same box: uncapped (32
-// waves per CU, the register limit) 0.947 ms; 26 per CU 0.942; 20 0.918;
-// 17-16 0.9135; 15-14 0.917; 13-12 0.950-0.986; 8 1.18 ms.  Wave priority and
-// the write-through stores still add 1-3 % on top of the cap.
-// The triples with 16-bit moments move fewer bytes per element for the same
-// arithmetic and conversions, and need the waves to hide it: at the C2 shape,
-// (bf16, bf16, bf16) 0.865 ms capped at 16 waves against 0.581 uncapped,
-// (f16, f16, f16) 1.070 against 0.715, (f16, f16, f32) 0.964 against 0.834;
-// (bf16, bf16, f32) is best at 20 waves (8 KiB: 0.817 against 0.848 at 16 and
-// 0.853 uncapped).  The other triples keep 16.  LA_UPDATE_LDS_BYTES, when
-// defined, overrides the table for every triple.
+// workgroups (= waves) resident per CU at 160 KiB / (reserved bytes), 12 for
+// 13 KiB.  Fewer streams in flight at once keep the HBM row buffers busier.
+// Measured on MI355X, C2 layer, (f32, bf16, f32), same box, update kernel:
+// 16 waves per CU 0.918 ms, 14 0.918, 13 0.910, 12 0.906, 11 0.909, 10 0.927;
+// the same kernel with the wave index left in vector registers (descriptors
+// built there, every access in a readfirstlane loop) was best at 16 waves,
+// 0.917 ms.  Wave priority and the write-through stores still add 1-3 % on
+// top of the cap.
+// The best cap differs by triple: bytes per element and conversion work
+// differ, and so do the waves needed to hide them.  At the C2 shape, same box
+// (ms per launch at 16 / 13 / 12 / 10 waves per CU or uncapped):
+// (bf16, bf16, bf16) best at 20 waves (8 KiB, 0.580 against 0.594 uncapped,
+// 0.664 at 12); (f16, f16, f16) and (f16, f16, f32) best at 16 (10 KiB: 0.552
+// and 0.805, against 0.577 and 0.836 uncapped); (f32, f32, f32) best at 10
+// (16 KiB: 0.978 against 0.996 at 12); the others at 12.  LA_UPDATE_LDS_BYTES,
+// when defined, overrides the table for every triple.
 #ifdef LA_UPDATE_LDS_BYTES
 #define LA_UPDATE_LDS_OVERRIDE 1
 #else
 #define LA_UPDATE_LDS_OVERRIDE 0
-#define LA_UPDATE_LDS_BYTES 10240
+#define LA_UPDATE_LDS_BYTES 13312
 #endif
 static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
 
@@ -347,6 +350,18 @@ struct StepArgs {
     Coeffs k;
 };
 
+// The value of lane 0 of the wave, as a wave-uniform value.  The wave index is
+// the same in every lane, but the compiler cannot prove it from threadIdx.x;
+// without this it keeps the index in vector registers, builds the buffer
+// descriptors there, wraps every buffer access in a readfirstlane loop and
+// fetches the multi kernel's segment arguments with per-lane vector loads.
+__device__ __forceinline__ uint64_t wave_uniform(uint64_t x)
+{
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // One wave's run of 64 aligned groups (256 elements) of every stream, run w of
 // the call: loads, update, stores.  Each stream is addressed through a raw
 // buffer descriptor whose base is the run's first element (scalar registers)
@@ -415,7 +430,8 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     // per stream.  The grid is one-shot unless n exceeds LA_MAX_GRID runs.
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t nwaves = stride >> 6;
-    for (uint64_t w = tid >> 6; w * 64 < a.nvec; w += nwaves) update_run<TP, TG, TS>(a, w, lane, has_coef, coef);
+    for (uint64_t w = wave_uniform(tid >> 6); w * 64 < a.nvec; w += nwaves)
+        update_run<TP, TG, TS>(a, w, lane, has_coef, coef);
 
     // Elements outside the aligned groups: [0, head) and [head + 4*nvec, n).
     const uint64_t vec_end = a.head + a.nvec * kVec;
@@ -458,7 +474,7 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_multi_kernel(MultiArgs a)
 {
     const bool has_coef = a.coef != nullptr;
     const float coef = has_coef ? *a.coef : 1.0f;
-    const uint64_t w = (static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x) >> 6;
+    const uint64_t w = wave_uniform((static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t runs = a.run_begin[a.count];
     if (w < runs) {
@@ -685,24 +701,24 @@ int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes, 
 template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_bytes()
 {
     if (LA_UPDATE_LDS_OVERRIDE) return LA_UPDATE_LDS_BYTES;
-    if (std::is_same<TS, bf16_t>::value || std::is_same<TS, f16_t>::value) return 0;          // 16-bit moments
-    if (std::is_same<TP, f16_t>::value && std::is_same<TG, f16_t>::value) return 0;           // (f16, f16, f32)
-    if (std::is_same<TP, bf16_t>::value && std::is_same<TG, bf16_t>::value) return 8192;      // (bf16, bf16, f32)
+    if (std::is_same<TP, bf16_t>::value && std::is_same<TS, bf16_t>::value) return 8192;       // (bf16, bf16, bf16)
+    if (std::is_same<TP, f16_t>::value && std::is_same<TG, f16_t>::value) return 10240;       // (f16, f16, f16 / f32)
+    if (std::is_same<TP, float>::value && std::is_same<TG, float>::value) return 16384;       // (f32, f32, f32)
     return LA_UPDATE_LDS_BYTES;
 }
 
 // The multi kernel's waves first look up their segment and its arguments, a
-// latency that more resident waves hide better: at most 8 KiB (20 waves per
-// CU).  Measured on MI355X, a GPT-2 block's twelve tensors in one launch:
-// (f32, bf16, f32) 33.5 us at 16 waves, 32.5 at 20, 31.9 uncapped;
-// (f32, f32, f32) 32.3, 31.9, 34.1.  LA_MULTI_LDS_BYTES, when defined,
-// overrides it for every triple.
+// latency that more resident waves hide better: at most 10 KiB (16 waves per
+// CU).  Measured on MI355X, a GPT-2 block's twelve tensors in one launch,
+// (f32, bf16, f32), step_with_grad_views: 30.4 us at 16 waves, 31.2 at 20,
+// 32.1 at 12, 31.3 uncapped.  LA_MULTI_LDS_BYTES, when defined, overrides it
+// for every triple.
 template <typename TP, typename TG, typename TS> constexpr uint32_t multi_lds_bytes()
 {
 #ifdef LA_MULTI_LDS_BYTES
     return LA_MULTI_LDS_BYTES;
 #else
-    return update_lds_bytes<TP, TG, TS>() < 8192u ? update_lds_bytes<TP, TG, TS>() : 8192u;
+    return update_lds_bytes<TP, TG, TS>() < 10240u ? update_lds_bytes<TP, TG, TS>() : 10240u;
 #endif
 }
 
