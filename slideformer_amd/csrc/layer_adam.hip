@@ -8,9 +8,10 @@
 // Memory layout of a launch: lane L of a wave owns 4 consecutive elements, so
 // one wave instruction covers 256 consecutive elements of every stream
 // (16-byte fp32 accesses, 8-byte 16-bit accesses, all lane-contiguous).  The
-// grid is one-shot (one group of 4 per lane) up to 2^22 workgroups: on gfx950
-// the vector memory counter covers loads and stores alike, so a grid-stride
-// loop would make each trip wait for the previous trip's store acknowledgements.
+// grid is one-shot (one group of 4 per lane, one wave per workgroup) up to
+// 2^26 workgroups, 2^34 elements: on gfx950 the vector memory counter covers
+// loads and stores alike, so a grid-stride loop would make each trip wait for
+// the previous trip's store acknowledgements.
 // Loads and stores carry the nontemporal hint (every byte is touched once), and
 // the stores are device-scope, so they are written through the L2.
 //
