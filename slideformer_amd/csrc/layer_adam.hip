@@ -9,7 +9,7 @@
 // one wave instruction covers 256 consecutive elements of every stream
 // (16-byte fp32 accesses, 8-byte 16-bit accesses, all lane-contiguous).  The
 // grid is one-shot (one group of 4 per lane, one wave per workgroup) up to
-// 2^26 workgroups, 2^34 elements: on gfx950 the vector memory counter covers
+// 2^26 - 1 workgroups, 2^34 - 256 elements: on gfx950 the vector memory counter covers
 // loads and stores alike, so a grid-stride loop would make each trip wait for
 // the previous trip's store acknowledgements.
 // Loads and stores carry the nontemporal hint (every byte is touched once), and
@@ -52,9 +52,11 @@
 #ifndef LA_NORM_BLOCK
 #define LA_NORM_BLOCK 512
 #endif
-// Upper bound on update workgroups per launch (grid-stride beyond it).
+// Upper bound on update workgroups per launch (grid-stride beyond it).  The
+// dispatch packet holds the grid size in work-items as a 32-bit number, so
+// workgroups x LA_BLOCK must stay below 2^32.
 #ifndef LA_MAX_GRID
-#define LA_MAX_GRID (1 << 26)
+#define LA_MAX_GRID ((1 << 26) - 1)
 #endif
 // Upper bound on grad-norm stage-1 workgroups (= partials folded by stage 2).
 // Measured on MI355X over a 218M-element bf16 buffer (workgroup size x
@@ -108,6 +110,8 @@
 #define LA_UPDATE_LDS_BYTES 13312
 #endif
 static_assert(LA_BLOCK % 64 == 0, "workgroups are whole waves");
+static_assert(static_cast<unsigned long long>(LA_MAX_GRID) * LA_BLOCK <= 0xffffffffull,
+              "the grid size in work-items must fit the dispatch packet's 32 bits");
 
 namespace {
 
