@@ -38,7 +38,7 @@ from typing import Any, DefaultDict, Dict, Iterable, Optional, Sequence
 
 import torch
 
-from . import _lib
+from . import _lib, cpu_adam_compat
 
 _DTYPE_CODE = {torch.float32: _lib.LA_F32, torch.bfloat16: _lib.LA_BF16, torch.float16: _lib.LA_F16}
 _DTYPE_NAME = {torch.float32: "Float", torch.bfloat16: "BFloat16", torch.float16: "Half"}
@@ -95,6 +95,12 @@ class HostStreamer:
         self.handle = handle
         self._ws = {}
         self._host_ws = {}
+        # every tensor of a call that returned once queued, until the pipeline
+        # has completed it: the pipeline's own streams still read and write
+        # them, and a temporary the caller drops (a grad moved to the device,
+        # a clip coefficient of this step) must not go back to the caching
+        # allocator, which could hand its memory out on the caller's stream
+        self._in_flight = []
 
     def _bytes(self, key) -> int:
         return self.lib.la_pipeline_workspace_bytes(self.chunk, self.slots, *[int(k) for k in key])
@@ -135,6 +141,8 @@ class HostStreamer:
         base = ws.data_ptr()
         aligned = (base + 255) // 256 * 256
         stats = _lib.LaPipelineStats() if synchronize else None
+        if not synchronize:
+            self._in_flight.append((params, grads, exp_avg, exp_avg_sq, bf16_out, clip_coef))
         rc = self.lib.la_pipeline_step(
             self.handle, ctypes.byref(scalars), pc, params.data_ptr(), gc, grads.data_ptr(), sc,
             exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n, None if bf16_out is None else bf16_out.data_ptr(),
@@ -142,11 +150,15 @@ class HostStreamer:
             ws.numel() - (aligned - base), stream_handle, int(synchronize),
             None if stats is None else ctypes.byref(stats))
         _lib.check(rc, "la_pipeline_step")
+        if synchronize:
+            # a synchronizing call completes every earlier call as well
+            self._in_flight.clear()
         return stats
 
     def sync(self):
         """Wait until every queued step is complete in host memory."""
         _lib.check(self.lib.la_pipeline_sync(self.handle), "la_pipeline_sync")
+        self._in_flight.clear()
 
     def __del__(self):
         try:
@@ -156,7 +168,10 @@ class HostStreamer:
             pass
 
 
-_ids = itertools.count()
+# LayerAdam ids start far above 0: the reference's own LayerAdam, run on the
+# cpu_adam stand-in of this package (cpu_adam_compat), always uses id 0
+# (layer_adam.py:62), and the two must not reset each other's state
+_ids = itertools.count(1 << 20)
 _ids_lock = threading.Lock()
 
 
@@ -304,8 +319,11 @@ class LayerAdam:
         ``overlap_host_chunks``: host-tensor updates return once queued, so that
         the runtime's one ``step_chunk`` per chunk keeps the host link busy across
         calls; ``end_chunk_step``, the end of ``step``/``step_with_grad_views`` and
-        ``synchronize()`` complete them.  Between those points the host tensors
-        passed in must not be read, written or freed."""
+        ``synchronize()`` complete them.  Between those points the tensors
+        passed in, host and device alike (grads, moments in HBM, ``bf16_out``,
+        ``clip_coef``), must not be read or written by the caller; the optimizer
+        keeps a reference to each of them until its update is complete, so a
+        temporary the caller drops is not freed early."""
         self.defaults = dict(
             lr=lr,
             bias_correction=bias_correction,
@@ -324,14 +342,17 @@ class LayerAdam:
             raise ValueError("moments_hbm_bytes needs moments_device and must be >= 0")
 
         # The reference loads its CPU extension here (layer_adam.py:59); this
-        # loads the HIP library and fails loudly if it is missing.
+        # loads the HIP library and fails loudly if it is missing.  cpu_adam is
+        # the module with the reference extension's three functions.
         self.lib = _lib.load()
+        self.cpu_adam = cpu_adam_compat
         # The reference always uses id 0 (layer_adam.py:62), so a second
         # instance would reset the first one's beta-power state; each instance
         # here gets its own id, and a single instance behaves identically.
         self.optimizer_id = _next_id()
-        _lib.check(self.lib.la_create(self.optimizer_id, lr, betas[0], betas[1], eps, weight_decay,
-                                      int(bool(adamw_mode)), 0), "la_create")
+        # creation logged, as layer_adam.py:63-72 asks for
+        self.cpu_adam.create_adam(self.optimizer_id, lr, betas[0], betas[1], eps, weight_decay,
+                                  adamw_mode, True)
 
         self.fp32_optimizer_state = fp32_optimizer_state
         self.num_layer = num_layer
@@ -473,6 +494,10 @@ class LayerAdam:
             self._load_layer(layer_idx - 1)
         else:
             self._load_layer(layer_idx)
+            # layer_adam.py:234-236 returns with this read still running, and the
+            # step that follows would read moments the read is still writing;
+            # the read is fenced here instead
+            self.offloader.sync_read_events()
 
     def _post_step(self, layer_idx: int):
         if self.offloader is None:

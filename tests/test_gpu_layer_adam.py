@@ -428,8 +428,7 @@ def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path)
         for idx in range(L_ - 1, -1, -1):
             g = torch.from_numpy(rng.normal(0, 1e-3, sizes[idx]).astype(np.float32)).bfloat16()
             group = adam.begin_chunk_step(idx)
-            if not prefetch:
-                adam.offloader.sync_read_events()
+            # prefetch=False: begin_chunk_step itself fences the layer's read
             assert adam.exp_avg_flat[idx].untyped_storage().nbytes() == sizes[idx] * 4
             adam.step_chunk(params[idx].data, g.to(hip_device), adam.exp_avg_flat[idx],
                             adam.exp_avg_sq_flat[idx], group)
@@ -573,6 +572,59 @@ def test_overlapped_host_chunks_in_the_runtime_protocol(pinned, hip_device):
                    g16="bf16")
     adam.synchronize()
     check()
+
+
+@pytest.mark.parametrize("pinned", [True, False])
+def test_overlapped_calls_keep_device_temporaries_alive(pinned, hip_device):
+    """overlap_host_chunks=True with the device inputs of each call as
+    temporaries the caller drops at once: per-chunk grads moved to the device
+    by the call expression, a clip coefficient recomputed every step and a
+    bf16 copy allocated per chunk.  After each call the caller allocates and
+    fills same-sized tensors on its stream, which would take over those blocks
+    if the optimizer let them go before the pipeline's own streams were done
+    with them.  Host master, moments in HBM.  Bit-exact with the oracle."""
+    from slideformer_amd.layer_adam import HostStreamer
+    n, call = 40_000, 7_000
+    rng = np.random.default_rng(80 + int(pinned))
+    p0 = rng.normal(0, 0.02, n).astype(np.float32)
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, overlap_host_chunks=True, moments_device=hip_device)
+    adam._streamers[hip_device] = HostStreamer(hip_device, chunk_elems=2048, slots=3)
+    master = torch.from_numpy(p0.copy())
+    if pinned:
+        master = master.pin_memory()
+    adam.add_layer_params(0, [torch.nn.Parameter(master)])
+    m, v = adam.exp_avg_flat[0], adam.exp_avg_sq_flat[0]
+    assert m.is_cuda and not master.is_cuda
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    ph, mh, vh = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    copies = []
+    for _ in range(3):
+        g = torch.from_numpy(rng.normal(0, 1e-2, n).astype(np.float32)).bfloat16()
+        gb = H.to_np_bits(g, "bf16")
+        c_ref, _ = O.clip_coef(O.grad_sqnorm(gb, "bf16"), 0.05)
+        group = adam.begin_chunk_step(0)
+        for cs in range(0, n, call):
+            ce = min(n, cs + call)
+            coef, _ = adam.clip_grad_norm([g.to(hip_device)], 0.05)
+            out = torch.empty(ce - cs, dtype=torch.bfloat16, device=hip_device)
+            adam.step_chunk(master[cs:ce], g[cs:ce].to(hip_device), m[cs:ce], v[cs:ce], group,
+                            bf16_out=out, clip_coef=coef)
+            copies.append((cs, ce, out))
+            del coef, out
+            # fresh allocations of the same sizes on the caller's stream, filled at once
+            for k in range(4):
+                torch.full((ce - cs,), float("nan"), dtype=torch.bfloat16, device=hip_device)
+                torch.full((1,), float("nan"), dtype=torch.float32, device=hip_device)
+            orc.update(group["step"], 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[cs:ce], gb[cs:ce], mh[cs:ce],
+                       vh[cs:ce], g16="bf16", clip_coef=float(np.float32(c_ref)))
+        adam.end_chunk_step(0)
+        assert not adam._streamers[hip_device]._in_flight     # released once complete
+        assert np.array_equal(master.numpy().view(np.uint32), ph.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(m, "f32"), mh.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(v, "f32"), vh.view(np.uint32))
+        for cs, ce, out in copies:
+            assert np.array_equal(H.to_np_bits(out, "bf16"), O.f32_to_bf16(ph[cs:ce])), (cs, ce)
+        copies.clear()
 
 
 # which of p, m, v, g and the bf16 copy are in host memory (the rest in HBM)
