@@ -269,16 +269,48 @@ int orc_adam_update(orc_adam_t* s, uint64_t step, float lr, float b1, float b2, 
 /* Compensated (Neumaier) float64 sum of the exact squares, so that the result
  * is the true sum to about one ulp of binary64 whatever the length; any
  * summation order (the GPU's tree) is then compared against the exact value. */
-double orc_grad_sqnorm(int g_dtype, const void* g, uint64_t n)
+/* Neumaier's compensated addition of y into the running pair (s, c). */
+static void neumaier_add(double* s, double* c, double y)
+{
+    const double t = *s + y;
+    if (fabs(*s) >= fabs(y)) *c += (*s - t) + y;
+    else *c += (y - t) + *s;
+    *s = t;
+}
+
+/* Compensated float64 sum of g[i]^2 over [lo, hi) as the pair (s, c). */
+static void sqnorm_block(int g_dtype, const void* g, uint64_t lo, uint64_t hi, double* s_out, double* c_out)
 {
     double s = 0.0, c = 0.0;
-    for (uint64_t i = 0; i < n; ++i) {
-        double x = (double)load_as_f32(g_dtype, g, i);
-        double y = x * x;  /* exact in binary64 for any binary32 x */
-        double t = s + y;
-        if (fabs(s) >= fabs(y)) c += (s - t) + y;
-        else c += (y - t) + s;
-        s = t;
+    for (uint64_t i = lo; i < hi; ++i) {
+        const double x = (double)load_as_f32(g_dtype, g, i);
+        neumaier_add(&s, &c, x * x);  /* x * x is exact in binary64 for any binary32 x */
+    }
+    *s_out = s;
+    *c_out = c;
+}
+
+/* Sum of squares, compensated.  Large inputs are cut into a fixed number of
+ * blocks summed in parallel; the blocks' pairs are then added, compensated, in
+ * block order, so the result does not depend on the thread count. */
+#define ORC_SQNORM_BLOCKS 64
+double orc_grad_sqnorm(int g_dtype, const void* g, uint64_t n)
+{
+    double s, c;
+    if (n < (1u << 20)) {
+        sqnorm_block(g_dtype, g, 0, n, &s, &c);
+        return s + c;
+    }
+    double bs[ORC_SQNORM_BLOCKS], bc[ORC_SQNORM_BLOCKS];
+#pragma omp parallel for schedule(static)
+    for (int b = 0; b < ORC_SQNORM_BLOCKS; ++b)
+        sqnorm_block(g_dtype, g, n / ORC_SQNORM_BLOCKS * (uint64_t)b,
+                     b == ORC_SQNORM_BLOCKS - 1 ? n : n / ORC_SQNORM_BLOCKS * (uint64_t)(b + 1), &bs[b], &bc[b]);
+    s = 0.0;
+    c = 0.0;
+    for (int b = 0; b < ORC_SQNORM_BLOCKS; ++b) {
+        neumaier_add(&s, &c, bs[b]);
+        neumaier_add(&s, &c, bc[b]);
     }
     return s + c;
 }

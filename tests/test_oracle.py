@@ -319,13 +319,21 @@ def test_f16_rne_matches_numpy():
     assert np.array_equal(back, ours[finite][:4096].view(np.float16).astype(np.float32))
 
 
-def test_sqnorm_is_exact_float64_sum():
+@pytest.mark.parametrize("n", [100001, 3_000_017])
+def test_sqnorm_is_exact_float64_sum(n):
+    # 3 M elements take the blocked parallel path; outliers x100 and a wide
+    # dynamic range make plain float64 accumulation visibly inexact
     rng = np.random.default_rng(5)
-    g = torch.from_numpy(rng.normal(0, 1e-3, 100001).astype(np.float32)).bfloat16()
+    x = rng.normal(0, 1e-3, n).astype(np.float32)
+    x[rng.integers(0, n, n // 1000)] *= 100
+    x[: n // 7] *= 1e-6
+    g = torch.from_numpy(x).bfloat16()
     gb = _np_bits(g, "bf16")
     got = O.grad_sqnorm(gb, "bf16")
-    exact = math.fsum(float(x) * float(x) for x in g.float().numpy())
-    assert abs(got - exact) <= 1e-12 * exact
+    exact = math.fsum(float(v) * float(v) for v in g.float().numpy())
+    assert abs(got - exact) <= 1e-15 * exact
+    # the same value in fp32 and fp16 storage
+    assert abs(O.grad_sqnorm(g.float().numpy().copy()) - exact) <= 1e-15 * exact
 
 
 def test_clip_coef_matches_torch_clip_grad_norm():
