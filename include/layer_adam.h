@@ -9,6 +9,7 @@
  * Return codes: 0 on success; LA_EINVAL for a null/misaligned pointer, an
  * unknown id or a bad size; LA_EDTYPE for a dtype triple the reference does
  * not register; LA_ENOMEM when host memory or a host thread cannot be had;
+ * LA_ERANGE for a size beyond the fixed scratch of la_grad_norm_clip_noalloc;
  * a positive hipError_t value when a HIP call fails.  No C++ exception
  * leaves the library.
  * All device entry points are asynchronous on the stream passed in.
@@ -23,12 +24,13 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 5
+#define LA_ABI_VERSION 6
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
 #define LA_EDTYPE (-95)
 #define LA_ENOMEM (-12)
+#define LA_ERANGE (-34)
 
 /* element types of p / g / m,v */
 #define LA_F32 0
@@ -152,6 +154,26 @@ int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, void* workspace,
 int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace,
                       uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm,
                       float* coef, float* norm_out, la_stream_t stream);
+
+/*
+ * la_grad_norm_clip without a workspace: for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The stage-1
+ * partials go to a fixed device array inside the library of
+ * LA_NORM_SCRATCH_PARTIALS float64 (2 KiB), one copy per GPU, held until the
+ * process ends; its address is looked up once per device.  The call itself
+ * allocates nothing (no hipMalloc, no hipFree, no allocating library call).
+ * Stage 1 of this build never uses more than 256 workgroups, so every n fits;
+ * a build whose stage-1 grid could outgrow the array returns LA_ERANGE for
+ * such n.  Runs on the current device; `stream` must belong to it.  Every
+ * call on one GPU shares that GPU's array, which keeps the last call's
+ * partials: calls that overlap on one GPU (streams not ordered with each
+ * other) race.  The results are bit-identical to la_grad_norm_clip's for the
+ * same arguments.
+ */
+#define LA_NORM_SCRATCH_PARTIALS 256
+int la_grad_norm_clip_noalloc(int g_dtype, const void* g, uint64_t n, double* sqnorm, int accumulate,
+                              float max_norm, float* coef, float* norm_out, la_stream_t stream);
 
 /*
  * Clip coefficient on device, torch.nn.utils.clip_grad_norm_ convention:

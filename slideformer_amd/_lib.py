@@ -21,6 +21,7 @@ LA_OK = 0
 LA_EINVAL = -22
 LA_EDTYPE = -95
 LA_ENOMEM = -12
+LA_ERANGE = -34
 
 LA_F32, LA_BF16, LA_F16 = 0, 1, 2
 
@@ -41,6 +42,7 @@ EXPORTED = (
     "la_grad_sqnorm_workspace",
     "la_grad_sqnorm",
     "la_grad_norm_clip",
+    "la_grad_norm_clip_noalloc",
     "la_clip_coef",
     "la_pipeline_workspace_bytes",
     "la_pipeline_create",
@@ -137,6 +139,8 @@ def _declare(L):
     L.la_grad_sqnorm.restype = i
     L.la_grad_norm_clip.argtypes = [i, P, u64, P, u64, P, i, f, P, P, P]
     L.la_grad_norm_clip.restype = i
+    L.la_grad_norm_clip_noalloc.argtypes = [i, P, u64, P, i, f, P, P, P]
+    L.la_grad_norm_clip_noalloc.restype = i
     L.la_clip_coef.argtypes = [P, f, P, P, P]
     L.la_clip_coef.restype = i
     L.la_pipeline_workspace_bytes.argtypes = [u64, i, i, i, i, ctypes.c_uint]

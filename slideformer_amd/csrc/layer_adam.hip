@@ -914,6 +914,43 @@ int launch_norm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_
 
 }  // namespace
 
+// Fixed device scratch of la_grad_norm_clip_noalloc: the grad norm's stage-1
+// partials (one float64 per stage-1 workgroup), for callers that cannot
+// allocate device memory.  Every GPU the library runs on holds its own copy
+// until the process ends.  Host code never uses this name as an address: on
+// the host it is only a stand-in, and the device address comes from
+// hipGetSymbolAddress (scratch_on_current_device below).
+static __device__ __align__(256) double scratch[LA_NORM_SCRATCH_PARTIALS];
+
+namespace {
+
+constexpr uint64_t kScratchBytes = static_cast<uint64_t>(LA_NORM_SCRATCH_PARTIALS) * sizeof(double);
+
+std::mutex g_scratch_mu;
+std::unordered_map<int, double*> g_scratch_ptr;  // device ordinal -> that device's copy of `scratch`
+
+// The address of `scratch` on the current device, looked up once per device
+// with that device current.
+int scratch_on_current_device(double** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_rc(e);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(dev);
+    if (it == g_scratch_ptr.end()) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_rc(e);
+        if (!ptr) return LA_EINVAL;
+        it = g_scratch_ptr.emplace(dev, static_cast<double*>(ptr)).first;
+    }
+    *out = it->second;
+    return LA_OK;
+}
+
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
@@ -927,6 +964,7 @@ const char* la_strerror(int code)
     if (code == LA_EINVAL) return "invalid argument (null/misaligned pointer, unknown id or bad size)";
     if (code == LA_EDTYPE) return "dtype triple not supported";
     if (code == LA_ENOMEM) return "out of host memory or host threads";
+    if (code == LA_ERANGE) return "size beyond the fixed device scratch of a no-allocation entry point";
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
     return "unknown error";
 }
@@ -1096,6 +1134,21 @@ int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace, u
     if (!coef) return LA_EINVAL;
     return launch_norm(g_dtype, g, n, workspace, workspace_bytes, sqnorm, accumulate, max_norm, coef, norm_out,
                        static_cast<hipStream_t>(stream));
+}
+
+int la_grad_norm_clip_noalloc(int g_dtype, const void* g, uint64_t n, double* sqnorm, int accumulate,
+                              float max_norm, float* coef, float* norm_out, la_stream_t stream)
+try {
+    if (!coef) return LA_EINVAL;
+    // stage 1 writes one partial per workgroup into the fixed array
+    if (norm_workspace_bytes(n) > kScratchBytes) return LA_ERANGE;
+    double* ptr = nullptr;
+    const int rc = scratch_on_current_device(&ptr);
+    if (rc != LA_OK) return rc;
+    return launch_norm(g_dtype, g, n, ptr, kScratchBytes, sqnorm, accumulate, max_norm, coef, norm_out,
+                       static_cast<hipStream_t>(stream));
+} catch (...) {
+    return LA_ENOMEM;
 }
 
 int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_out, la_stream_t stream)

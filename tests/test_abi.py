@@ -36,9 +36,9 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
-    assert L.la_abi_version() == version == 5
+    assert L.la_abi_version() == version == 6
     header = _read(HEADER)
-    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
+    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
                  "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):
         value = int(re.search(rf"#define {name} \(?(-?\d+)u?\)?", header).group(1))
         assert getattr(_lib, name) == value, name
@@ -119,6 +119,9 @@ def test_error_codes_without_launch():
     assert L.la_grad_sqnorm(1, None, 10, None, 0, None, 0, None) == _lib.LA_EINVAL
     assert L.la_grad_norm_clip(1, None, 10, None, 0, None, 0, 1.0, None, None, None) == _lib.LA_EINVAL
     assert L.la_clip_coef(None, 1.0, None, None, None) == _lib.LA_EINVAL
+    # the no-allocation norm checks coef before it looks anything up on a device
+    assert L.la_grad_norm_clip_noalloc(1, None, 10, None, 0, 1.0, None, None, None) == _lib.LA_EINVAL
+    assert b"scratch" in L.la_strerror(_lib.LA_ERANGE)
     assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
     assert b"memory" in L.la_strerror(_lib.LA_ENOMEM)
 
