@@ -40,15 +40,24 @@ def log(msg: str) -> None:
 
 
 def read_traffic():
-    """HBM bytes per update launch from the committed rocprofv3 --pmc summary, if any."""
+    """(HBM bytes per update launch, where they come from) from the committed
+    rocprofv3 --pmc summary, or (None, None).  The counters are not read in this
+    run: the figure holds for the kernel build the summary names."""
+    value, build = None, None
     try:
         with open(TRAFFIC_SUMMARY) as fh:
             for line in fh:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
+                    value = float(line.split(":", 1)[1])
+                elif line.startswith("kernel_build:"):
+                    build = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    if value is None:
+        return None, None
+    source = (f"{os.path.relpath(TRAFFIC_SUMMARY, REPO)}: rocprofv3 --pmc sized L2 read/write request "
+              f"counters (TCC_EA0_RDREQ_128B/64B/32B, TCC_EA0_WRREQ/WRREQ_64B), kernel build {build}")
+    return value, source
 
 
 def cpu_baseline(n: int, budget_s: float):
@@ -888,7 +897,7 @@ def main():
     value = n / (ms_per_step * 1e-3) / 1e9
     achieved = BYTES_PER_PARAM_UPDATE * n / (upd_avg * 1e-3) / 1e9
     step_bytes = (BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0)) * n
-    traffic = read_traffic()
+    traffic, traffic_source = read_traffic()
 
     result = {
         "metric": METRIC,
@@ -924,6 +933,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "la_adamw_kernel<float, bf16_t, float>",
             "algorithmic_bytes_per_launch": BYTES_PER_PARAM_UPDATE * n,
         },
