@@ -135,6 +135,52 @@ def cpu_baseline(n: int, budget_s: float):
     }
 
 
+def link_ceiling(dev, bytes_each_way, chunk_bytes, slots=3, reps=2):
+    """The host link alone, from page-locked memory in the pipeline's chunk
+    size: H2D alone, D2H alone, and both at once on two streams (the duplex
+    ceiling a streamed step can reach), each moving bytes_each_way per
+    direction.  Returns (h2d_ms, d2h_ms, duplex_ms) per pass."""
+    import torch
+
+    elems = chunk_bytes // 4
+    src_h = torch.empty(slots * elems, dtype=torch.float32, pin_memory=True)
+    dst_h = torch.empty(slots * elems, dtype=torch.float32, pin_memory=True)
+    dev_in = torch.empty(slots * elems, dtype=torch.float32, device=dev)
+    dev_out = torch.zeros(slots * elems, dtype=torch.float32, device=dev)
+    copies = -(-bytes_each_way // chunk_bytes)
+    sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    cur = torch.cuda.current_stream(dev)
+
+    def issue(h2d, d2h):
+        for i in range(copies):
+            k = i % slots
+            if h2d:
+                with torch.cuda.stream(sa):
+                    dev_in[k * elems:(k + 1) * elems].copy_(src_h[k * elems:(k + 1) * elems], non_blocking=True)
+            if d2h:
+                with torch.cuda.stream(sb):
+                    dst_h[k * elems:(k + 1) * elems].copy_(dev_out[k * elems:(k + 1) * elems], non_blocking=True)
+
+    def timed(h2d, d2h):
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(cur)
+        sa.wait_stream(cur)
+        sb.wait_stream(cur)
+        for _ in range(reps):
+            issue(h2d, d2h)
+        cur.wait_stream(sa)
+        cur.wait_stream(sb)
+        stop.record(cur)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / reps
+
+    timed(True, True)  # warm-up
+    out = (timed(True, False), timed(False, True), timed(True, True))
+    del src_h, dst_h, dev_in, dev_out
+    return out
+
+
 C5_LAYER = [12288 * 3 * 12288, 3 * 12288, 12288 * 12288, 12288, 12288 * 49152, 49152, 49152 * 12288, 12288,
             12288, 12288, 12288, 12288]  # qkv(+b), o(+b), fc1(+b), fc2(+b), 2 LayerNorms (w, b)
 
@@ -269,6 +315,10 @@ def streamed(args):
     t_comp = timed(lambda: adam.step_chunk(pd, gd, md, vd, dict(adam.defaults, step=args.warmup + args.steps + 1),
                                            bf16_out=out))
     del pd, md, vd, gd
+    # the link alone, page-locked, the pipeline's chunk size: the duplex ceiling
+    link_h2d, link_d2h, link_duplex = link_ceiling(dev, d2h_bytes, chunk * 4)
+    log(f"link alone, page-locked, {d2h_bytes / 1e9:.2f} GB each way in {chunk * 4 >> 20} MiB copies: "
+        f"H2D {link_h2d:.2f} ms, D2H {link_d2h:.2f} ms, both at once {link_duplex:.2f} ms")
     res = {
         "metric": "streamed LayerAdam step (host-resident fp32 state), Gparams/s",
         "value": round(n / (wall * 1e-3) / 1e9, 3),
@@ -294,7 +344,20 @@ def streamed(args):
         "h2d_gbs_isolated": round(h2d_bytes / (t_h2d * 1e-3) / 1e9, 2),
         "d2h_gbs_isolated": round(d2h_bytes / (t_d2h * 1e-3) / 1e9, 2),
         "isolated_ms": {"h2d": round(t_h2d, 3), "update": round(t_comp, 3), "d2h": round(t_d2h, 3)},
-        "overlap": round((t_h2d + t_d2h + t_comp) / wall, 3),
+        # sum of isolated stage times / wall; only where the isolated copies are
+        # the pipeline's own kind (page-locked): pageable isolated copies take the
+        # HIP runtime's bounce buffers, which the staged pipeline does not use
+        "overlap": round((t_h2d + t_d2h + t_comp) / wall, 3) if not args.pageable else None,
+        "link_ceiling": {
+            "what": (f"the host link alone: page-locked hipMemcpyAsync of {d2h_bytes} B each way in "
+                     f"{chunk * 4} B copies, H2D and D2H on two streams at once (duplex) and each alone"),
+            "h2d_alone_gbs": round(d2h_bytes / (link_h2d * 1e-3) / 1e9, 2),
+            "d2h_alone_gbs": round(d2h_bytes / (link_d2h * 1e-3) / 1e9, 2),
+            "duplex_each_way_gbs": round(d2h_bytes / (link_duplex * 1e-3) / 1e9, 2),
+            "duplex_ms": round(link_duplex, 3),
+            # the fraction of the duplex ceiling the streamed step reaches (same bytes each way)
+            "pipeline_efficiency": round(link_duplex / wall, 4) if not args.host_grads else None,
+        },
         "stream_spans_ms": ({"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
                              "d2h": round(st.d2h_ms, 3)} if st is not None and call == n else None),
     }

@@ -75,19 +75,26 @@
 #ifndef LA_NT_LOAD
 #define LA_NT_LOAD 1
 #endif
-// The grad-norm kernel's loads are plain (no nontemporal hint), so the grads
-// it reads stay in the 256 MB memory-side cache (MALL) for the update that
-// follows; the update's own nontemporal traffic does not displace them.  The
-// grid walks the buffer from the top down, so the front of the buffer, which
-// the update's first waves read, is the part read last.  Measured on MI355X,
-// C2 layer (436 MB of bf16 grads), norm then update, per step: nontemporal
-// ascending 0.986 ms (update 0.919), nontemporal descending 0.987 (0.920),
-// plain ascending 0.958 (0.886), plain descending 0.957 (0.885); the norm pass
+// The grad-norm kernel's loads.  A call that also writes the clip coefficient
+// (la_grad_norm_clip) is the last read of these grads before the update that
+// uses the coefficient: its loads are plain (no nontemporal hint), so the
+// grads it reads stay in the 256 MB memory-side cache (MALL) for that update,
+// whose own nontemporal traffic does not displace them.  The grid walks the
+// buffer from the top down, so the front of the buffer, which the update's
+// first waves read, is the part read last.  Measured on MI355X, C2 layer
+// (436 MB of bf16 grads), norm then update, per step: nontemporal ascending
+// 0.986 ms (update 0.919), nontemporal descending 0.987 (0.920), plain
+// ascending 0.958 (0.886), plain descending 0.957 (0.885); the norm pass
 // itself takes ~4 us longer with plain loads.  Loading only the front 160-320
 // MiB plain and the rest nontemporal, or folding the partials with one wave
 // instead of eight, changed the step by less than 1 us.
-#ifndef LA_NORM_NT_LOAD
-#define LA_NORM_NT_LOAD 0
+// A call that only accumulates (la_grad_sqnorm: one layer of a global norm,
+// whose update waits for every other layer's norm) keeps the nontemporal
+// hint: there the grads would not stay cached until their update, and the
+// plain loads only cost time (whole resident models, 34-48 layers: 219
+// instead of 222 Gparams/s with plain loads everywhere).
+#ifndef LA_NORM_CLIP_PLAIN
+#define LA_NORM_CLIP_PLAIN 1
 #endif
 #ifndef LA_NORM_DESCENDING
 #define LA_NORM_DESCENDING 1
@@ -583,15 +590,14 @@ struct NormArgs {
     float* norm_out;      // may be null
 };
 
-template <typename TG>
+template <typename TG, bool NT>
 __global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
 {
     const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_NORM_BLOCK + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_NORM_BLOCK;
-    constexpr bool kNt = LA_NORM_NT_LOAD != 0;
     // aligned group i of the walk -> group index in the buffer
     auto group = [&a](uint64_t i) { return LA_NORM_DESCENDING ? a.nvec - 1 - i : i; };
-    auto load = [&a](uint64_t gidx, float (&x)[kVec]) { Io<TG>::template load4<kNt>(a.g, a.head + gidx * kVec, x); };
+    auto load = [&a](uint64_t gidx, float (&x)[kVec]) { Io<TG>::template load4<NT>(a.g, a.head + gidx * kVec, x); };
     double acc = 0.0;
     uint64_t gi = tid;
     for (; gi + (LA_NORM_UNROLL - 1) * stride < a.nvec; gi += LA_NORM_UNROLL * stride) {
@@ -922,11 +928,22 @@ int launch_norm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_
     a.max_norm = max_norm;
     a.coef = coef;
     a.norm_out = norm_out;
+    // plain loads for the read that produces the coefficient, nontemporal otherwise
+    const bool nt = !(coef && LA_NORM_CLIP_PLAIN);
     int rc;
     switch (g_dtype) {
-    case LA_F32: rc = launch(la_sqnorm_kernel<float>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
-    case LA_BF16: rc = launch(la_sqnorm_kernel<bf16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
-    default: rc = launch(la_sqnorm_kernel<f16_t>, dim3(grid), dim3(LA_NORM_BLOCK), 0, st, a); break;
+    case LA_F32:
+        rc = launch(nt ? la_sqnorm_kernel<float, true> : la_sqnorm_kernel<float, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, a);
+        break;
+    case LA_BF16:
+        rc = launch(nt ? la_sqnorm_kernel<bf16_t, true> : la_sqnorm_kernel<bf16_t, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, a);
+        break;
+    default:
+        rc = launch(nt ? la_sqnorm_kernel<f16_t, true> : la_sqnorm_kernel<f16_t, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, a);
+        break;
     }
     if (rc != LA_OK) return rc;
     return launch(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);

@@ -40,6 +40,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <new>
@@ -51,6 +52,17 @@
 
 using la_host::CopyPool;
 using la_host::Piece;
+
+// Host-side trace of the pipeline's HIP calls, off in the product build:
+// with LA_PIPELINE_TRACE defined to 1, every call of la_pipeline_step that
+// holds the calling thread for LA_PIPELINE_TRACE_MS or longer is printed to
+// stderr with its pipeline call, chunk, slot and text.
+#ifndef LA_PIPELINE_TRACE
+#define LA_PIPELINE_TRACE 0
+#endif
+#ifndef LA_PIPELINE_TRACE_MS
+#define LA_PIPELINE_TRACE_MS 0.5
+#endif
 
 struct la_pipeline {
     int device = 0;
@@ -77,6 +89,7 @@ struct la_pipeline {
     // layout can overlap slot s + 1 of this one
     const char* last_ws = nullptr;
     uint64_t last_slot_bytes = 0;
+    uint64_t calls = 0;  // la_pipeline_step calls so far (the trace's call numbers)
 };
 
 namespace {
@@ -411,11 +424,30 @@ try {
         return LA_OK;
     };
 
+    uint64_t trace_chunk = 0, trace_slot = 0;
+    const uint64_t trace_call = pl->calls++;
+    (void)trace_chunk;
+    (void)trace_slot;
+    (void)trace_call;
+#if LA_PIPELINE_TRACE
+#define LA_STEP_TRY(expr)                                                                                        \
+    do {                                                                                                         \
+        const auto a_ = std::chrono::steady_clock::now();                                                        \
+        const hipError_t e_ = (expr);                                                                            \
+        const double ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - a_).count(); \
+        if (ms_ >= LA_PIPELINE_TRACE_MS)                                                                         \
+            std::fprintf(stderr, "[la_pipeline] call %llu chunk %llu slot %llu: %.3f ms in %s\n",                \
+                         (unsigned long long)trace_call, (unsigned long long)trace_chunk,                         \
+                         (unsigned long long)trace_slot, ms_, #expr);                                            \
+        if (e_ != hipSuccess) return drain_streams(pl, rc_of(e_));                                                \
+    } while (0)
+#else
 #define LA_STEP_TRY(expr)                                         \
     do {                                                          \
         const hipError_t e_ = (expr);                             \
         if (e_ != hipSuccess) return drain_streams(pl, rc_of(e_)); \
     } while (0)
+#endif
 
     // Everything the caller queued before (e.g. the backward that produced g)
     // comes first.  A call that stages pageable arrays waits for it on the host
@@ -439,6 +471,8 @@ try {
 
     for (uint64_t i = 0; i < nchunks; ++i) {
         const uint64_t s = pl->issued % S;
+        trace_chunk = i;
+        trace_slot = s;
         const uint64_t off = i * pl->chunk;
         const uint64_t k = (n - off) < pl->chunk ? (n - off) : pl->chunk;
         char* slot = ws + s * L.slot_bytes;
