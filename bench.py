@@ -497,7 +497,7 @@ def streamed_model(args):
     crosses the link."""
     import torch
 
-    from slideformer_amd import LayerAdam
+    from slideformer_amd import LayerAdam, _lib
     from slideformer_amd.layer_adam import HostStreamer
 
     dev = torch.device("cuda", 0)
@@ -513,8 +513,18 @@ def streamed_model(args):
     adam._streamers[dev] = HostStreamer(dev, chunk_elems=chunk, slots=slots, host_threads=args.host_threads)
     params, grads, outs = [], [], []
     piece = 256 * 1024 * 1024
+    # page-locked state per segment, in sliding order (the first segments stepped),
+    # while the --pin-gib budget lasts; the rest stays pageable and is staged
+    pinned = set()
+    budget = int(args.pin_gib * (1 << 30))
+    per_param = 4 if args.moments_in_hbm else 12
+    for idx in range(len(sizes) - 1, -1, -1):
+        if per_param * sizes[idx] <= budget:
+            budget -= per_param * sizes[idx]
+            pinned.add(idx)
     for idx, n in enumerate(sizes):
-        p = torch.empty(n, dtype=torch.float32)
+        adam.pin_host_state = idx in pinned        # read by add_layer_params for the moments
+        p = _lib.page_locked_empty(n, torch.float32) if idx in pinned else torch.empty(n, dtype=torch.float32)
         for lo in range(0, n, piece):
             hi = min(n, lo + piece)
             p[lo:hi].copy_(torch.randn(hi - lo, generator=gen, device=dev) * 0.02)
@@ -568,6 +578,20 @@ def streamed_model(args):
         workload = workload.replace("fp32 p/m/v in pageable host RAM (the reference's allocation)",
                                     "fp32 master in pageable host RAM (the reference's allocation), "
                                     "fp32 moments in HBM")
+    if pinned:
+        pinned_params = sum(sizes[i] for i in pinned)
+        where = (f"page-locked at exact size ({per_param * pinned_params / 2**30:.1f} GiB; one process may "
+                 f"page-lock at most 64 GiB on this host)")
+        if len(pinned) < len(sizes):
+            where = (f"page-locked for {len(pinned)} of {len(sizes)} segments (the first {len(pinned)} in sliding "
+                     f"order, {pinned_params} params, {per_param * pinned_params / 2**30:.1f} GiB at exact size; one "
+                     f"process may page-lock at most 64 GiB on this host), pageable for the rest")
+        workload = workload.replace("in pageable host RAM (the reference's allocation)", where)
+        if len(pinned) == len(sizes):
+            workload = workload.replace(", staged through page-locked slot twins by native host threads", "")
+        else:
+            workload = workload.replace("staged through page-locked slot twins",
+                                        "the pageable ones staged through page-locked slot twins")
     res = {
         "metric": "streamed LayerAdam full-model step (host-resident fp32 state), Gparams/s",
         "value": round(n_total / wall / 1e9, 3),
@@ -580,7 +604,8 @@ def streamed_model(args):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": workload, "moments": "HBM" if args.moments_in_hbm else "host",
-                   "params": n_total, "layers": len(sizes), "chunk_elems": chunk, "slots": slots},
+                   "params": n_total, "layers": len(sizes), "chunk_elems": chunk, "slots": slots,
+                   "page_locked_segments": sorted(pinned)},
         "h2d_gbs_effective": round(each_way / wall / 1e9, 2),
         "d2h_gbs_effective": round(each_way / wall / 1e9, 2),
         "bytes_each_way_per_step": each_way,
@@ -839,6 +864,9 @@ def main():
                     help="with --streamed c3-layer|c5: pipeline chunk in Mi elements (default: the config's)")
     ap.add_argument("--slots", type=int, default=0,
                     help="with --streamed c3-layer|c5: pipeline slots (default: the config's)")
+    ap.add_argument("--pin-gib", type=float, default=0.0,
+                    help="with --streamed c3: page-lock the host state of whole segments, in sliding order, up "
+                         "to this many GiB (the rest stays pageable and is staged)")
     ap.add_argument("--triples", action="store_true",
                     help="time the update kernel on every registered dtype triple at the C2 shape")
     ap.add_argument("--copy-ceiling", action="store_true",

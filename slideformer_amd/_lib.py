@@ -11,7 +11,9 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import weakref
 
+import numpy as np
 import torch  # noqa: F401  (binds the HIP runtime before the library is loaded)
 
 # where slideformer_amd/build.py writes the library
@@ -190,3 +192,69 @@ def check(rc: int, what: str) -> None:
     if rc != LA_OK:
         msg = load().la_strerror(rc).decode()
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+_hip_runtime = None
+
+
+def _hip():
+    """The HIP runtime torch has loaded (the same soname resolves to it)."""
+    global _hip_runtime
+    with _lock:
+        if _hip_runtime is None:
+            rt = ctypes.CDLL("libamdhip64.so")
+            rt.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+            rt.hipHostMalloc.restype = ctypes.c_int
+            rt.hipHostFree.argtypes = [ctypes.c_void_p]
+            rt.hipHostFree.restype = ctypes.c_int
+            _hip_runtime = rt
+        return _hip_runtime
+
+
+# start address -> bytes of every live page_locked_empty allocation
+_page_locked = {}
+
+
+def _release(rt, address: int) -> None:
+    with _lock:
+        _page_locked.pop(address, None)
+    rt.hipHostFree(address)
+
+
+def is_page_locked(t: torch.Tensor) -> bool:
+    """Whether a host tensor lies in page-locked memory: torch's own pinned
+    blocks (``is_pinned``) or a ``page_locked_empty`` allocation, which torch
+    does not recognise as pinned."""
+    if t.is_cuda:
+        return False
+    if t.is_pinned():
+        return True
+    ptr = t.data_ptr()
+    with _lock:
+        return any(start <= ptr < start + size for start, size in _page_locked.items())
+
+
+def page_locked_empty(numel: int, dtype: torch.dtype) -> torch.Tensor:
+    """A host tensor of exactly ``numel`` elements in page-locked memory
+    (one ``hipHostMalloc``), uninitialised.
+
+    torch's pinned allocator (``pin_memory=True``) rounds every allocation up to
+    a power of two: an 872 MB moment of a Llama-3.1-8B layer takes 1 GiB, a
+    2.1 GB vocab matrix 4 GiB.  A process may page-lock only so much host
+    memory (64 GiB on the MI355X hosts measured), so exact sizes fit more
+    state.  The memory is released with ``hipHostFree`` once the last tensor
+    that views it is gone.  torch's ``is_pinned()`` reports False for it;
+    ``is_page_locked()`` knows it."""
+    elem = torch.empty(0, dtype=dtype).element_size()
+    nbytes = numel * elem
+    rt = _hip()
+    ptr = ctypes.c_void_p()
+    rc = rt.hipHostMalloc(ctypes.byref(ptr), max(1, nbytes), 0)
+    if rc != 0 or not ptr.value:
+        raise RuntimeError(f"hipHostMalloc of {nbytes} bytes failed (hipError_t {rc})")
+    raw = np.frombuffer((ctypes.c_uint8 * max(1, nbytes)).from_address(ptr.value), dtype=np.uint8)
+    with _lock:
+        _page_locked[ptr.value] = max(1, nbytes)
+    weakref.finalize(raw, _release, rt, ptr.value)
+    return torch.from_numpy(raw)[:nbytes].view(dtype)
+

@@ -137,7 +137,7 @@ class HostStreamer:
         key = (pc, gc, sc, on_host)
         ws = self.workspace(*key)
         host = [t for t in (params, grads, exp_avg, exp_avg_sq, bf16_out) if t is not None and not t.is_cuda]
-        self._attach_host_staging(key, self.stage_pageable and not all(t.is_pinned() for t in host))
+        self._attach_host_staging(key, self.stage_pageable and not all(_lib.is_page_locked(t) for t in host))
         base = ws.data_ptr()
         aligned = (base + 255) // 256 * 256
         stats = _lib.LaPipelineStats() if synchronize else None
@@ -313,9 +313,10 @@ class LayerAdam:
         may take (None = no limit); layers registered once it is used up keep
         their moments beside their params, so a model whose moments do not all
         fit in HBM keeps as many layers' moments there as the budget allows;
-        ``pin_host_state``: allocate host-resident moments in page-locked memory
-        (streamed without staging copies; the reference allocates pageable memory,
-        which the pipeline stages through page-locked buffers);
+        ``pin_host_state``: allocate host-resident moments in page-locked memory,
+        at their exact size (streamed without staging copies; the reference
+        allocates pageable memory, which the pipeline stages through page-locked
+        buffers);
         ``overlap_host_chunks``: host-tensor updates return once queued, so that
         the runtime's one ``step_chunk`` per chunk keeps the host link busy across
         calls; ``end_chunk_step``, the end of ``step``/``step_with_grad_views`` and
@@ -443,12 +444,16 @@ class LayerAdam:
         self.param_groups.append(param_group)
         # host moments are page-locked on request: the copy engines then read and
         # write them directly, without the staging copies that pageable arrays
-        # take (not with the file offload, which releases and re-allocates them)
+        # take (not with the file offload, which releases and re-allocates them);
+        # at their exact size, since a process may page-lock only so much
         pin = (device.type == 'cpu' and self.pin_host_state and self.offloader is None
                and torch.cuda.is_available())
-        self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device, pin_memory=pin)
-        self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device,
-                                                      pin_memory=pin)
+        if pin:
+            self.exp_avg_flat[layer_idx] = _lib.page_locked_empty(layer_numel, state_type).zero_()
+            self.exp_avg_sq_flat[layer_idx] = _lib.page_locked_empty(layer_numel, state_type).zero_()
+        else:
+            self.exp_avg_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
+            self.exp_avg_sq_flat[layer_idx] = torch.zeros(layer_numel, dtype=state_type, device=device)
         if device == self.moments_device:
             self.moments_hbm_used += need
         offset = 0

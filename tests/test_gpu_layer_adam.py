@@ -448,6 +448,35 @@ def test_nvme_offload_in_sliding_order(fraction, prefetch, hip_device, tmp_path)
             assert np.array_equal(adam.exp_avg_sq_flat[idx].numpy().view(np.uint32), v_h[idx].view(np.uint32))
 
 
+def test_page_locked_empty_is_exact_and_page_locked(hip_device):
+    """_lib.page_locked_empty: one hipHostMalloc of exactly the bytes asked for
+    (torch's pinned allocator would round 872 MB up to 1 GiB), seen as
+    page-locked by torch and by the pipeline, usable as a copy source and
+    target, and released with its last tensor."""
+    import gc
+
+    from slideformer_amd import _lib
+    n = 218_112_000 // 64 + 5                       # not a power of two
+    t = _lib.page_locked_empty(n, torch.float32)
+    assert t.numel() == n and t.untyped_storage().nbytes() == 4 * n and _lib.is_page_locked(t)
+    assert _lib.is_page_locked(t[n // 2:]) and not _lib.is_page_locked(torch.empty(n))
+    t.copy_(torch.arange(n, dtype=torch.float32))
+    d = t.to(hip_device, non_blocking=True)
+    back = _lib.page_locked_empty(n, torch.float32)
+    back.copy_(d * 2, non_blocking=True)
+    torch.cuda.synchronize()
+    assert torch.equal(back, torch.arange(n, dtype=torch.float32) * 2)
+    assert _lib.page_locked_empty(0, torch.bfloat16).numel() == 0
+    del t, back
+    gc.collect()
+    # the same amount again, many times over: the earlier buffers were released
+    for _ in range(8):
+        x = _lib.page_locked_empty(1 << 28, torch.uint8)   # 256 MiB
+        assert _lib.is_page_locked(x)
+        del x
+        gc.collect()
+
+
 def test_pinned_host_state_layer_step(hip_device):
     """pin_host_state=True: add_layer_params allocates page-locked host moments;
     step(layer) on host params streams them; bit-exact with the oracle."""
@@ -456,7 +485,8 @@ def test_pinned_host_state_layer_step(hip_device):
     x = rng.normal(0, 0.02, 50_003).astype(np.float32)
     p = torch.nn.Parameter(torch.from_numpy(x.copy()))
     adam.add_layer_params(0, [p])
-    assert adam.exp_avg_flat[0].is_pinned() and adam.exp_avg_sq_flat[0].is_pinned()
+    from slideformer_amd import _lib
+    assert _lib.is_page_locked(adam.exp_avg_flat[0]) and _lib.is_page_locked(adam.exp_avg_sq_flat[0])
     m_h, v_h = np.zeros_like(x), np.zeros_like(x)
     orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
     for step in (1, 2):
@@ -541,7 +571,8 @@ def test_overlapped_host_chunks_in_the_runtime_protocol(pinned, hip_device):
         master = master.pin_memory()
     adam.add_layer_params(0, [torch.nn.Parameter(master)])
     m, v = adam.exp_avg_flat[0], adam.exp_avg_sq_flat[0]
-    assert m.is_pinned() == pinned and master.is_pinned() == pinned
+    from slideformer_amd import _lib
+    assert _lib.is_page_locked(m) == pinned and master.is_pinned() == pinned
     orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
     ph, mh, vh = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
 

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from slideformer_amd import LayerAdam
+from slideformer_amd import LayerAdam, _lib
 from tests import _hip as H
 
 pytestmark = pytest.mark.gpu
@@ -121,7 +121,7 @@ def test_c3_model_sliding_order_from_page_locked_state(hip_device):
         assert adam.add_layer_params(pos[idx], [torch.nn.Parameter(p_h)]) == pos[idx]
         assert resident.add_layer_params(pos[idx], [torch.nn.Parameter(p_d)]) == pos[idx]
         m_h, v_h = adam.exp_avg_flat[pos[idx]], adam.exp_avg_sq_flat[pos[idx]]
-        assert m_h.is_pinned() and v_h.is_pinned() and p_h.is_pinned()
+        assert _lib.is_page_locked(m_h) and _lib.is_page_locked(v_h) and p_h.is_pinned()
         m_h.copy_(m_d)
         v_h.copy_(v_d)
         resident.exp_avg_flat[pos[idx]].copy_(m_d)

@@ -239,3 +239,9 @@ def test_offload_cleanup_leaves_other_processes_files(tmp_path):
     gc.collect()
     assert list(tmp_path.glob(f"offload-{os.getpid()}-*")) == []
     assert foreign.read_bytes() == b"another run's moments"
+
+
+def test_is_page_locked_of_plain_host_memory():
+    from slideformer_amd import _lib
+    assert not _lib.is_page_locked(torch.zeros(16))
+    assert not _lib.is_page_locked(torch.zeros(16)[4:])
