@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 6
+#define LA_ABI_VERSION 7
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -280,10 +280,19 @@ int la_pipeline_step(la_pipeline_t* pl, const la_scalars_t* sc, int p_dtype, voi
  *     A read of a key never written returns -ENOENT.
  *   la_disk_sync_writes / la_disk_sync_reads: wait for every queued write /
  *     read; return 0 or the first failure as a negative errno.
+ *   la_disk_create_ex with LA_DISK_DIRECT: the files are opened with O_DIRECT
+ *     (no page-cache copies; the device's rates).  Buffers need no alignment:
+ *     pieces of 16 MiB, unaligned ones through an aligned bounce buffer per
+ *     worker, the last piece padded with zeros to a 4 KiB block.  Returns
+ *     the open() error (e.g. -EINVAL) when the directory's file system does
+ *     not take O_DIRECT.  la_disk_create is la_disk_create_ex with flags 0.
  */
 typedef struct la_disk la_disk_t;
 
+#define LA_DISK_DIRECT 1u
+
 int la_disk_create(const char* dir, int threads, la_disk_t** out);
+int la_disk_create_ex(const char* dir, int threads, unsigned flags, la_disk_t** out);
 int la_disk_destroy(la_disk_t* d);
 int la_disk_write_async(la_disk_t* d, uint64_t key, const void* src, uint64_t bytes);
 int la_disk_read_async(la_disk_t* d, uint64_t key, void* dst, uint64_t bytes);

@@ -31,6 +31,9 @@ LA_F32, LA_BF16, LA_F16 = 0, 1, 2
 LA_ON_HOST_P, LA_ON_HOST_M, LA_ON_HOST_V, LA_ON_HOST_G, LA_ON_HOST_OUT = 1, 2, 4, 8, 16
 LA_ON_HOST_ALL = 31
 
+# la_disk_create_ex flags
+LA_DISK_DIRECT = 1
+
 # every exported symbol of include/layer_adam.h
 EXPORTED = (
     "la_abi_version",
@@ -53,6 +56,7 @@ EXPORTED = (
     "la_pipeline_set_host_staging",
     "la_pipeline_step",
     "la_disk_create",
+    "la_disk_create_ex",
     "la_disk_destroy",
     "la_disk_write_async",
     "la_disk_read_async",
@@ -160,6 +164,8 @@ def _declare(L):
     L.la_pipeline_step.restype = i
     L.la_disk_create.argtypes = [ctypes.c_char_p, i, ctypes.POINTER(P)]
     L.la_disk_create.restype = i
+    L.la_disk_create_ex.argtypes = [ctypes.c_char_p, i, ctypes.c_uint, ctypes.POINTER(P)]
+    L.la_disk_create_ex.restype = i
     L.la_disk_destroy.argtypes = [P]
     L.la_disk_destroy.restype = i
     L.la_disk_write_async.argtypes = [P, u64, P, u64]

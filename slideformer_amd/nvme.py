@@ -9,11 +9,24 @@ complete after ``sync_read_events()``.  Views into the buffer (LayerAdam's
 per-parameter ``state`` views) stay valid across the release/re-allocation
 because they share the storage object.  The I/O runs on the native worker
 pool of ``libslideformer_amd.so`` (``la_disk_*``).
+
+``backend`` names tensornvme's I/O engine in the reference (it passes
+``'uring'``, layer_adam.py:101).  io_uring itself is not used here: the pool's
+threads issue positioned reads and writes.  The name selects how they reach
+the file:
+  * ``'uring'``, ``'aio'``, ``'direct'``: direct I/O (``O_DIRECT``).  The
+    moments leave host RAM for real, instead of staying in it as cached
+    pages, and the rates are the device's.  If the directory's file system
+    refuses ``O_DIRECT``, buffered I/O is used instead, with a warning
+    (``self.direct`` tells which);
+  * ``'pthread'``, ``'buffered'``: buffered I/O through the page cache.
 """
 from __future__ import annotations
 
 import ctypes
+import errno
 import os
+import warnings
 from typing import Dict, List, Set
 
 import torch
@@ -22,16 +35,27 @@ from . import _lib
 
 
 class DiskOffloader:
+    DIRECT_BACKENDS = ('uring', 'aio', 'direct')
+    BUFFERED_BACKENDS = ('pthread', 'buffered')
+
     def __init__(self, dir_name: str, n_entries: int = 16, backend: str = 'uring'):
-        # `backend` names tensornvme's I/O engine; here every backend is the
-        # native thread pool, `n_entries` bounds its size.
+        # `n_entries` bounds the size of the native thread pool
+        if backend not in self.DIRECT_BACKENDS + self.BUFFERED_BACKENDS:
+            raise ValueError(f"unknown backend {backend!r}; one of {self.DIRECT_BACKENDS + self.BUFFERED_BACKENDS}")
         self.lib = _lib.load()
         self.dir_name = os.path.abspath(dir_name)
         os.makedirs(self.dir_name, exist_ok=True)
         self.backend = backend
+        threads = max(1, min(int(n_entries), 16))
         handle = ctypes.c_void_p()
-        rc = self.lib.la_disk_create(self.dir_name.encode(), max(1, min(int(n_entries), 16)),
-                                     ctypes.byref(handle))
+        self.direct = backend in self.DIRECT_BACKENDS
+        rc = self.lib.la_disk_create_ex(self.dir_name.encode(), threads, _lib.LA_DISK_DIRECT if self.direct else 0,
+                                        ctypes.byref(handle))
+        if self.direct and rc == -errno.EINVAL:
+            warnings.warn(f"{self.dir_name}: the file system does not take O_DIRECT; offloading through the "
+                          "page cache instead", RuntimeWarning, stacklevel=2)
+            self.direct = False
+            rc = self.lib.la_disk_create_ex(self.dir_name.encode(), threads, 0, ctypes.byref(handle))
         if rc != 0:
             raise OSError(-rc, f"la_disk_create({self.dir_name}) failed: {os.strerror(-rc) if rc < 0 else rc}")
         self.handle = handle

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
-    assert L.la_abi_version() == version == 6
+    assert L.la_abi_version() == version == 7
     header = _read(HEADER)
     for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
                  "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):

@@ -102,11 +102,14 @@ def test_argument_checks_precede_dispatch():
         adam.adam_update(1, 1e-3, 0.9, 0.999, 1e-8, 0, True, a, a, a.to("meta"), a)
 
 
-def test_disk_offloader_round_trip(tmp_path):
+@pytest.mark.parametrize("backend", ["uring", "pthread"])
+def test_disk_offloader_round_trip(backend, tmp_path):
     """Native file offload (la_disk_*), the contract LayerAdam uses
-    (layer_adam.py:200-247): write, release, read back bit-identical."""
+    (layer_adam.py:200-247): write, release, read back bit-identical; with
+    direct I/O ('uring', the reference's backend) and buffered I/O."""
     from slideformer_amd.nvme import DiskOffloader
-    off = DiskOffloader(str(tmp_path), 4, 'uring')
+    off = DiskOffloader(str(tmp_path), 4, backend)
+    assert off.direct == (backend == 'uring')
     a = torch.randn(17 * (1 << 20) + 7)         # 68 MB: two 64 MiB I/O pieces
     b = torch.arange(1000, dtype=torch.float32)
     a_copy, b_copy = a.clone(), b.clone()
@@ -245,3 +248,62 @@ def test_is_page_locked_of_plain_host_memory():
     from slideformer_amd import _lib
     assert not _lib.is_page_locked(torch.zeros(16))
     assert not _lib.is_page_locked(torch.zeros(16)[4:])
+
+
+def test_disk_offloader_backends_and_direct_fallback(tmp_path, monkeypatch):
+    """backend names: 'uring' / 'aio' / 'direct' ask for O_DIRECT, 'pthread' /
+    'buffered' for the page cache, anything else is refused.  A file system
+    that refuses O_DIRECT (-EINVAL at create) falls back to buffered I/O with a
+    warning, and the offload still round-trips."""
+    import errno
+
+    from slideformer_amd import _lib
+    from slideformer_amd.nvme import DiskOffloader
+    with pytest.raises(ValueError, match="unknown backend"):
+        DiskOffloader(str(tmp_path), 2, 'io_uring_sqpoll')
+    assert DiskOffloader(str(tmp_path), 2, 'aio').direct and not DiskOffloader(str(tmp_path), 2, 'buffered').direct
+
+    real = _lib.load()
+
+    class RefusesDirect:
+        def __getattr__(self, name):
+            return getattr(real, name)
+
+        def la_disk_create_ex(self, d, threads, flags, out):
+            if flags & _lib.LA_DISK_DIRECT:
+                return -errno.EINVAL
+            return real.la_disk_create_ex(d, threads, flags, out)
+
+    monkeypatch.setattr(_lib, "load", lambda path=None: RefusesDirect())
+    with pytest.warns(RuntimeWarning, match="O_DIRECT"):
+        off = DiskOffloader(str(tmp_path), 2, 'uring')
+    assert not off.direct
+    a = torch.arange(5003, dtype=torch.float32)
+    ref = a.clone()
+    off.async_write(a)
+    off.sync_write_events()
+    off.async_read(a)
+    off.sync_read_events()
+    assert torch.equal(a, ref)
+    del off
+
+
+def test_disk_offloader_direct_mode_odd_sizes_and_alignments(tmp_path):
+    """Direct I/O with host tensors of sizes that are not whole blocks (the
+    bounce buffer and the zero-padded last block; the block-aligned path is
+    driven by tests/native/disk_offload_driver.cpp): every byte comes back."""
+    from slideformer_amd.nvme import DiskOffloader
+    off = DiskOffloader(str(tmp_path), 4, 'direct')
+    assert off.direct
+    tensors = [torch.randn(k) for k in (1, 3, 1023, 4 * (1 << 20) + 1, 5 * (1 << 20) + 777)]
+    tensors.append(torch.randint(0, 255, (4097,), dtype=torch.uint8))
+    refs = [t.clone() for t in tensors]
+    for t in tensors:
+        off.async_write(t)
+    off.sync_write_events()
+    for t in tensors:
+        off.async_read(t)
+    off.sync_read_events()
+    for t, r in zip(tensors, refs):
+        assert torch.equal(t, r)
+
