@@ -261,6 +261,9 @@ def page_locked_empty(numel: int, dtype: torch.dtype) -> torch.Tensor:
     raw = np.frombuffer((ctypes.c_uint8 * max(1, nbytes)).from_address(ptr.value), dtype=np.uint8)
     with _lock:
         _page_locked[ptr.value] = max(1, nbytes)
-    weakref.finalize(raw, _release, rt, ptr.value)
+    # Not at interpreter exit: finalizers then run in no fixed order, possibly
+    # before a pipeline that still copies into this memory has been drained;
+    # the process's own teardown reclaims it.
+    weakref.finalize(raw, _release, rt, ptr.value).atexit = False
     return torch.from_numpy(raw)[:nbytes].view(dtype)
 
