@@ -444,7 +444,11 @@ def triples(args):
     stream = torch.cuda.current_stream(dev)
     names = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
     rows = []
-    for pd, gd, sd in SUPPORTED_TRIPLES:
+    order = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+    only = set(args.triple_filter.split(",")) if args.triple_filter else None
+    for pd, gd, sd in sorted(SUPPORTED_TRIPLES, key=lambda t: tuple(order[x] for x in t)):
+        if only is not None and "/".join(names[x] for x in (pd, gd, sd)) not in only:
+            continue
         gen = torch.Generator(device=dev)
         gen.manual_seed(20)
         p = (torch.randn(n, generator=gen, device=dev) * 0.02).to(pd)
@@ -908,6 +912,8 @@ def main():
                          "to this many GiB (the rest stays pageable and is staged)")
     ap.add_argument("--triples", action="store_true",
                     help="time the update kernel on every registered dtype triple at the C2 shape")
+    ap.add_argument("--triple-filter", default="",
+                    help="with --triples: only these triples, e.g. bf16/bf16/bf16,f16/f16/f16")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain HBM copies of one C2 update's bytes beside the update kernel")
     ap.add_argument("--moments-in-hbm", action="store_true",

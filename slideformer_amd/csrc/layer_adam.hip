@@ -470,6 +470,98 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw_kernel(StepArgs a)
     }
 }
 
+// All-16-bit triples ((bf16, bf16, bf16), (f16, f16, f16)): every stream, the
+// bf16 copy included, has 2-byte elements, so a lane owns 8 consecutive
+// elements and moves each stream with one 16-byte access; one wave
+// instruction covers 512 elements (1 KiB) of a stream, and a launch needs
+// half the waves of the 4-element layout.  The per-element arithmetic and the
+// scalar path are the same as la_adamw_kernel's.  `head` and `nvec` of the
+// arguments count 8-element groups here.
+constexpr int kVec16 = 8;
+
+template <typename Conv> struct WaveIo16x8 {
+    __device__ __forceinline__ static rsrc_t rsrc(const void* base, uint64_t e0, uint32_t nel)
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(static_cast<const uint16_t*>(base) + e0), 0,
+                                                 static_cast<int>(nel * 2), kRsrcFlags);
+    }
+    __device__ __forceinline__ static void load8(rsrc_t r, uint32_t lane, float (&x)[kVec16])
+    {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(lane * 16), 0, kAux);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = Conv::to_f32(w[k] & 0xffffu);
+            x[2 * k + 1] = Conv::to_f32(w[k] >> 16);
+        }
+    }
+    __device__ __forceinline__ static void store8(rsrc_t r, uint32_t lane, const float (&x)[kVec16])
+    {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = Conv::from_f32(x[2 * k]) | (Conv::from_f32(x[2 * k + 1]) << 16);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, static_cast<int>(lane * 16), 0,
+                                               kAuxSt);
+    }
+};
+template <typename T> struct Conv16;
+template <> struct Conv16<bf16_t> { using type = ConvBf16; };
+template <> struct Conv16<f16_t> { using type = ConvF16; };
+
+template <typename T16, typename TG16>
+__device__ __forceinline__ void update_run16(const StepArgs& a, uint64_t w, uint32_t lane, bool has_coef, float coef)
+{
+    using IoS = WaveIo16x8<typename Conv16<T16>::type>;
+    using IoG = WaveIo16x8<typename Conv16<TG16>::type>;
+    const uint64_t left = a.nvec - w * 64;
+    const uint32_t nel = (left < 64 ? static_cast<uint32_t>(left) : 64u) * kVec16;
+    const uint64_t e0 = a.head + w * 64 * kVec16;
+    const rsrc_t rg = IoG::rsrc(a.g, e0, nel);
+    const rsrc_t rp = IoS::rsrc(a.p, e0, nel);
+    const rsrc_t rm = IoS::rsrc(a.m, e0, nel);
+    const rsrc_t rv = IoS::rsrc(a.v, e0, nel);
+    float p[kVec16], g[kVec16], m[kVec16], v[kVec16];
+#if LA_SETPRIO
+    __builtin_amdgcn_s_setprio(3);
+#endif
+    IoG::load8(rg, lane, g);
+    IoS::load8(rp, lane, p);
+    IoS::load8(rm, lane, m);
+    IoS::load8(rv, lane, v);
+#if LA_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+#pragma unroll
+    for (int j = 0; j < kVec16; ++j) {
+        const float gj = has_coef ? g[j] * coef : g[j];
+        adam_body(p[j], gj, m[j], v[j], a.k);
+    }
+    IoS::store8(rp, lane, p);
+    IoS::store8(rm, lane, m);
+    IoS::store8(rv, lane, v);
+    if (a.out) WaveIo16x8<ConvBf16>::store8(WaveIo16x8<ConvBf16>::rsrc(a.out, e0, nel), lane, p);
+}
+
+template <typename TP, typename TG, typename TS>
+__global__ __launch_bounds__(LA_BLOCK) void la_adamw16_kernel(StepArgs a)
+{
+    static_assert(std::is_same<TP, TS>::value && std::is_same<TP, TG>::value, "all-16-bit triples only");
+    const bool has_coef = a.coef != nullptr;
+    const float coef = has_coef ? *a.coef : 1.0f;
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_BLOCK;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t nwaves = stride >> 6;
+    for (uint64_t w = wave_uniform(tid >> 6); w * 64 < a.nvec; w += nwaves)
+        update_run16<TP, TG>(a, w, lane, has_coef, coef);
+    const uint64_t vec_end = a.head + a.nvec * kVec16;
+    const uint64_t nscalar = a.head + (a.n - vec_end);
+    for (uint64_t s = tid; s < nscalar; s += stride) {
+        const uint64_t e = s < a.head ? s : vec_end + (s - a.head);
+        update_one<TP, TG, TS>(a, e, has_coef, coef);
+    }
+}
+
 // Several calls of one step in one launch: the tensors of a layer, each its
 // own reference adam_update call with its own scalars (the beta-power state
 // advances once per call) and its own scalar tail.  Waves [run_begin[s],
@@ -674,15 +766,15 @@ std::unordered_map<int, HostState> g_states;
 int elem_bytes(int dt) { return dt == LA_F32 ? 4 : 2; }
 bool dt_valid(int dt) { return dt == LA_F32 || dt == LA_BF16 || dt == LA_F16; }
 
-// First element index h in [0, 4) at which every pointer is aligned to a full
-// group (4 elements: 16 bytes for fp32, 8 bytes for 16-bit types), or -1 when
-// the pointers disagree in phase.
-int common_head(const uintptr_t* addr, const int* bytes, int count)
+// First element index h in [0, vec) at which every pointer is aligned to a
+// full group of `vec` elements (4 elements: 16 bytes for fp32, 8 bytes for
+// 16-bit types), or -1 when the pointers disagree in phase.
+int common_head(const uintptr_t* addr, const int* bytes, int count, int vec = kVec)
 {
-    for (int h = 0; h < kVec; ++h) {
+    for (int h = 0; h < vec; ++h) {
         bool ok = true;
         for (int i = 0; i < count && ok; ++i) {
-            const uintptr_t align = static_cast<uintptr_t>(kVec * bytes[i]);
+            const uintptr_t align = static_cast<uintptr_t>(vec * bytes[i]);
             ok = ((addr[i] + static_cast<uintptr_t>(h) * bytes[i]) % align) == 0;
         }
         if (ok) return h;
@@ -738,6 +830,27 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_b
     return LA_UPDATE_LDS_BYTES;
 }
 
+// The all-16-bit path moves twice the bytes per wave, so it wants fewer
+// resident waves than the 4-element layout of the same triple.  Measured on
+// MI355X, C2 shape, 100 launches, three runs, ms per launch (4-element layout
+// at its own best cap / 8-element layout at 10, 11, 12, 13, 14 KiB reserved):
+// (bf16, bf16, bf16) 0.571-0.574 / 0.549-0.553, 0.547-0.551, 0.546-0.550,
+// 0.550-0.553, 0.560-0.561; (f16, f16, f16) 0.539-0.541 / 0.534-0.536,
+// 0.532-0.534, 0.531, 0.524-0.525, 0.524-0.526.  Kept: 12 KiB (13 waves per
+// CU) and 13 KiB (12).  LA_UPDATE16_LDS_BYTES, when defined, overrides both;
+// LA_WIDE16=0 restores the 4-element layout for these triples.
+#ifndef LA_WIDE16
+#define LA_WIDE16 1
+#endif
+template <typename T> constexpr uint32_t update16_lds_bytes()
+{
+#ifdef LA_UPDATE16_LDS_BYTES
+    return LA_UPDATE16_LDS_BYTES;
+#else
+    return std::is_same<T, bf16_t>::value ? 12288u : 13312u;
+#endif
+}
+
 // The multi kernel's waves first look up their segment and its arguments, a
 // latency that more resident waves hide better: at most 10 KiB (16 waves per
 // CU).  Measured on MI355X, a GPT-2 block's twelve tensors in one launch,
@@ -753,9 +866,35 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t multi_lds_by
 #endif
 }
 
+// The all-16-bit path: the call's groups are re-laid out as 8-element groups.
+template <typename T> int launch16(const StepArgs& a4, hipStream_t stream)
+{
+    StepArgs a = a4;
+    const uintptr_t addr[5] = {reinterpret_cast<uintptr_t>(a.p), reinterpret_cast<uintptr_t>(a.g),
+                               reinterpret_cast<uintptr_t>(a.m), reinterpret_cast<uintptr_t>(a.v),
+                               reinterpret_cast<uintptr_t>(a.out)};
+    const int bytes[5] = {2, 2, 2, 2, 2};
+    const int h = common_head(addr, bytes, a.out ? 5 : 4, kVec16);
+    if (h < 0 || static_cast<uint64_t>(h) >= a.tail_start) {
+        a.head = 0;
+        a.nvec = 0;
+    } else {
+        a.head = static_cast<uint64_t>(h);
+        a.nvec = (a.tail_start - a.head) / kVec16;
+    }
+    const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec16));
+    const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
+    const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
+    return launch(la_adamw16_kernel<T, T, T>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
+                  update16_lds_bytes<T>(), stream, a);
+}
+
 template <typename TP, typename TG, typename TS> struct StepLauncher {
     static int run(const StepArgs& a, hipStream_t stream)
     {
+        if constexpr (LA_WIDE16 && std::is_same<TP, TG>::value && std::is_same<TP, TS>::value &&
+                      !std::is_same<TP, float>::value)
+            return launch16<TP>(a, stream);
         const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
         // lanes needed: every wave takes one run of 64 groups
         const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;

@@ -191,6 +191,50 @@ def test_every_triple_and_mode(triple, mode, hip_device):
     assert G.same_bits(H.to_np_bits(vd, sk), vh, sk).all()
 
 
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+@pytest.mark.parametrize("offsets", [(0, 0, 0, 0, 0), (1, 1, 1, 1, 1), (3, 3, 3, 3, 3), (4, 4, 4, 4, 4),
+                                     (7, 7, 7, 7, 7), (0, 4, 0, 0, 0), (2, 2, 6, 2, 2), (5, 1, 3, 7, 0)])
+def test_all_16bit_triples_every_head_phase(kind, offsets, hip_device):
+    """The all-16-bit triples ((bf16, bf16, bf16), (f16, f16, f16)) run a kernel
+    whose lanes own 8 consecutive elements: the head that aligns every stream,
+    the bf16 copy included, to 8-element (16-byte) groups, the 512-element
+    runs, the remainder and the reference's scalar tail.  Every head phase
+    0-7, phases that agree only modulo 4 (then the whole call takes the scalar
+    path), sizes around 8, 16, 512 and the tail, with the bf16 copy and a clip
+    coefficient: every bit equals the oracle's."""
+    op, og, om, ov, oo = offsets
+    log(f"16-bit triple {kind} offsets {offsets}")
+    rng = np.random.default_rng(zlib.crc32(repr((kind, offsets)).encode()))
+    sizes = (1, 7, 8, 15, 16, 17, 511, 512, 513, 1023, 4099, 70_001, 100_003)
+    total = sum(sizes)
+    td = H.TD[kind]
+    P = torch.from_numpy(rng.normal(0, 0.02, total + 8).astype(np.float32)).to(td).to(hip_device)
+    M = torch.from_numpy(rng.normal(0, 1e-3, total + 8).astype(np.float32)).to(td).to(hip_device)
+    V = torch.from_numpy(np.abs(rng.normal(0, 1e-6, total + 8)).astype(np.float32)).to(td).to(hip_device)
+    OUT = torch.zeros(total + 8, dtype=torch.bfloat16, device=hip_device)
+    ph, mh, vh = H.to_np_bits(P, kind), H.to_np_bits(M, kind), H.to_np_bits(V, kind)
+    oh = np.zeros(total + 8, np.uint16)
+    coef = torch.tensor([0.625], device=hip_device)
+    opt = H.HipAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2):
+        g = torch.from_numpy(rng.normal(0, 1e-3, total + 8).astype(np.float32)).to(td)
+        gd, gh = g.to(hip_device), H.to_np_bits(g, kind)
+        lo = 0
+        for n in sizes:
+            opt.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, P[op + lo:op + lo + n], gd[og + lo:og + lo + n],
+                       M[om + lo:om + lo + n], V[ov + lo:ov + lo + n], out=OUT[oo + lo:oo + lo + n], coef=coef)
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, ph[op + lo:op + lo + n], gh[og + lo:og + lo + n],
+                       mh[om + lo:om + lo + n], vh[ov + lo:ov + lo + n], p16=kind, g16=kind, s16=kind,
+                       p_bf16_out=oh[oo + lo:oo + lo + n], clip_coef=0.625)
+            lo += n
+    torch.cuda.synchronize()
+    assert G.same_bits(H.to_np_bits(P, kind), ph, kind).all()
+    assert G.same_bits(H.to_np_bits(M, kind), mh, kind).all()
+    assert G.same_bits(H.to_np_bits(V, kind), vh, kind).all()
+    assert np.array_equal(H.to_np_bits(OUT, "bf16")[oo:oo + total], oh[oo:oo + total])
+
+
 def test_denormal_and_extreme_values(hip_device):
     """Subnormal v and grads, zero grads, huge grads: IEEE denormals are kept."""
     log("denormals")
