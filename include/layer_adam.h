@@ -10,6 +10,10 @@
  * unknown id or a bad size; LA_EDTYPE for a dtype triple the reference does
  * not register; LA_ENOMEM when host memory or a host thread cannot be had;
  * LA_ERANGE for a size beyond the fixed scratch of la_grad_norm_clip_noalloc;
+ * LA_EFAULT when an array a kernel would read or write (p, g, m, v, the bf16
+ * copy, the clip coefficient, the norm's scalars and workspace) is not device
+ * memory: host arrays, pageable or page-locked, are refused before any launch
+ * (la_pipeline_step streams them);
  * a positive hipError_t value when a HIP call fails.  No C++ exception
  * leaves the library.
  * All device entry points are asynchronous on the stream passed in.
@@ -24,13 +28,14 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 7
+#define LA_ABI_VERSION 8
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
 #define LA_EDTYPE (-95)
 #define LA_ENOMEM (-12)
 #define LA_ERANGE (-34)
+#define LA_EFAULT (-14)
 
 /* element types of p / g / m,v */
 #define LA_F32 0

@@ -24,6 +24,7 @@ LA_EINVAL = -22
 LA_EDTYPE = -95
 LA_ENOMEM = -12
 LA_ERANGE = -34
+LA_EFAULT = -14
 
 LA_F32, LA_BF16, LA_F16 = 0, 1, 2
 

@@ -139,6 +139,18 @@ bool page_locked(const void* ptr)
     return a.type == hipMemoryTypeHost;
 }
 
+// Device (or managed / unified) memory, which the update may read and write in place.
+bool device_memory(const void* ptr)
+{
+    hipPointerAttribute_t a;
+    std::memset(&a, 0, sizeof(a));
+    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged || a.type == hipMemoryTypeUnified;
+}
+
 // Host copies are split into pieces of at most this many bytes for the pool.
 constexpr uint64_t kPieceBytes = 1ull << 20;
 
@@ -350,6 +362,12 @@ try {
         return LA_EINVAL;
     if (clip_coef && misaligned(clip_coef, 4)) return LA_EINVAL;
     if (misaligned(workspace, static_cast<int>(kAlign))) return LA_EINVAL;
+    // arrays the update reads and writes in place must be device memory; refuse
+    // them here, before any transfer starts, rather than in the first chunk
+    if ((!hp && !device_memory(p)) || (!hm && !device_memory(m)) || (!hv && !device_memory(v)) ||
+        (!hg && !device_memory(g)) || (out && !ho && !device_memory(out)) || !device_memory(workspace) ||
+        (clip_coef && !device_memory(clip_coef)))
+        return LA_EFAULT;
     const SlotLayout L = slot_layout(pl->chunk, p_dtype, g_dtype, s_dtype, on_host);
     const uint64_t ws_need = L.slot_bytes * static_cast<uint64_t>(pl->slots);
     if (workspace_bytes < ws_need) return LA_EINVAL;

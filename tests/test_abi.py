@@ -36,9 +36,9 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
-    assert L.la_abi_version() == version == 7
+    assert L.la_abi_version() == version == 8
     header = _read(HEADER)
-    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
+    for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_EFAULT", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
                  "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):
         value = int(re.search(rf"#define {name} \(?(-?\d+)u?\)?", header).group(1))
         assert getattr(_lib, name) == value, name
@@ -122,6 +122,13 @@ def test_error_codes_without_launch():
     # the no-allocation norm checks coef before it looks anything up on a device
     assert L.la_grad_norm_clip_noalloc(1, None, 10, None, 0, 1.0, None, None, None) == _lib.LA_EINVAL
     assert b"scratch" in L.la_strerror(_lib.LA_ERANGE)
+    # aligned host memory handed to the device entry points: refused before any launch
+    host = np.zeros(64, np.float32)
+    hp = host.ctypes.data + (-host.ctypes.data) % 16
+    assert L.la_adamw_step(ctypes.byref(sc), 0, hp, 0, hp, 0, hp, hp, 8, None, None, None) == _lib.LA_EFAULT
+    assert L.la_grad_sqnorm(0, hp, 8, hp, 64, hp, 0, None) == _lib.LA_EFAULT
+    assert L.la_clip_coef(hp, 1.0, hp, None, None) == _lib.LA_EFAULT
+    assert b"device memory" in L.la_strerror(_lib.LA_EFAULT)
     assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
     assert b"memory" in L.la_strerror(_lib.LA_ENOMEM)
 
@@ -165,9 +172,15 @@ def test_multi_update_host_logic_without_launch():
     args = (904, 5, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, 0, 1, 0)
     assert L.la_adam_update_multi(*args, None, -1, None, None) == _lib.LA_EINVAL
     assert L.la_adam_update_multi(*args, None, 2, None, None) == _lib.LA_EINVAL
-    # a misaligned pointer in the second segment: rejected, nothing advanced
-    bad = _segments([(0x1000, 0x2000, 0x3000, 0x4000, None, 8), (0x1001, 0x2000, 0x3000, 0x4000, None, 8)])
-    assert L.la_adam_update_multi(*args, bad, 2, None, None) == _lib.LA_EINVAL
+    # a misaligned pointer: rejected, nothing advanced
+    bad = _segments([(0x1001, 0x2000, 0x3000, 0x4000, None, 8)])
+    assert L.la_adam_update_multi(*args, bad, 1, None, None) == _lib.LA_EINVAL
+    # aligned addresses that are not device memory (no GPU here, or host
+    # memory on a GPU box) in the second segment: rejected, nothing advanced
+    host = np.zeros(64, np.float32)
+    hp = host.ctypes.data + (-host.ctypes.data) % 16
+    bad = _segments([(None,) * 5 + (0,), (hp, hp, hp, hp, None, 4)])
+    assert L.la_adam_update_multi(*args, bad, 2, None, None) == _lib.LA_EFAULT
     # unknown id: nothing to advance
     assert L.la_adam_update_multi(123457, *args[1:], _segments([(None,) * 5 + (0,)]), 1, None, None) == _lib.LA_EINVAL
     # three empty segments: no launch, three state advances

@@ -1238,6 +1238,64 @@ def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     md = torch.zeros(n + 1, device=hip_device)
     assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V, mptr=md.data_ptr() + 2) == _lib.LA_EINVAL
     assert not md.any()
+    # exp_avg placed as device-resident but in host memory (page-locked, then
+    # pageable): refused before any transfer, not handed to the kernel
+    assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V) == _lib.LA_EFAULT
+    mh = torch.zeros(n)
+    assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V, mptr=mh.data_ptr()) == _lib.LA_EFAULT
     torch.cuda.synchronize()
-    assert torch.equal(p, p_before) and not m.any() and not v.any()
+    assert torch.equal(p, p_before) and not m.any() and not v.any() and not mh.any()
     L.la_destroy(77)
+
+
+def test_device_entry_points_refuse_host_memory(hip_device):
+    """The device entry points refuse host arrays, page-locked or pageable,
+    with LA_EFAULT before any launch: a host address in a kernel would fault
+    the GPU.  The beta-power state still advances, as for any bad argument
+    after la_scalars, and the host arrays are untouched."""
+    import ctypes
+
+    from slideformer_amd import _lib
+    L = _lib.load()
+    n = 4096
+    st = torch.cuda.current_stream(hip_device).cuda_stream
+    dev = [torch.zeros(n, device=hip_device) for _ in range(3)]
+    gd = torch.zeros(n, dtype=torch.bfloat16, device=hip_device)
+    L.la_create(78, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0)
+    for pinned in (True, False):
+        h = torch.randn(n)
+        if pinned:
+            h = h.pin_memory()
+        before = h.clone()
+        for k in range(4):      # the host array as p, m, v or g
+            arrs = [dev[0].data_ptr(), gd.data_ptr(), dev[1].data_ptr(), dev[2].data_ptr()]
+            if k == 1:
+                hb = h.bfloat16() if not pinned else h.bfloat16().pin_memory()
+                arrs[1] = hb.data_ptr()
+            else:
+                arrs[k] = h.data_ptr()
+            rc = L.la_adam_update(78, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, _lib.LA_F32, arrs[0], _lib.LA_BF16, arrs[1],
+                                  _lib.LA_F32, arrs[2], arrs[3], n, None, None, st)
+            assert rc == _lib.LA_EFAULT, (pinned, k, rc)
+        # the bf16 copy and the clip coefficient on the host
+        hb16 = torch.zeros(n, dtype=torch.bfloat16)
+        assert L.la_adam_update(78, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, _lib.LA_F32, dev[0].data_ptr(), _lib.LA_BF16,
+                                gd.data_ptr(), _lib.LA_F32, dev[1].data_ptr(), dev[2].data_ptr(), n,
+                                hb16.data_ptr(), None, st) == _lib.LA_EFAULT
+        coef_h = torch.ones(1)
+        assert L.la_adam_update(78, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, _lib.LA_F32, dev[0].data_ptr(), _lib.LA_BF16,
+                                gd.data_ptr(), _lib.LA_F32, dev[1].data_ptr(), dev[2].data_ptr(), n, None,
+                                coef_h.data_ptr(), st) == _lib.LA_EFAULT
+        # the grad norm and the clip coefficient on host memory
+        ws = torch.zeros(64, dtype=torch.float64, device=hip_device)
+        sq = torch.zeros(1, dtype=torch.float64, device=hip_device)
+        assert L.la_grad_sqnorm(_lib.LA_F32, h.data_ptr(), n, ws.data_ptr(), 512, sq.data_ptr(), 0, st) == _lib.LA_EFAULT
+        sq_h = torch.zeros(1, dtype=torch.float64)
+        assert L.la_clip_coef(sq_h.data_ptr(), 1.0, coef_h.data_ptr(), None, st) == _lib.LA_EFAULT
+        torch.cuda.synchronize()
+        assert torch.equal(h, before) and not hb16.any() and coef_h.item() == 1.0
+    # device arrays still work
+    assert L.la_adam_update(78, 2, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, _lib.LA_F32, dev[0].data_ptr(), _lib.LA_BF16,
+                            gd.data_ptr(), _lib.LA_F32, dev[1].data_ptr(), dev[2].data_ptr(), n, None, None, st) == 0
+    torch.cuda.synchronize()
+    L.la_destroy(78)
