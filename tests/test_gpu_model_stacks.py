@@ -67,8 +67,8 @@ def test_c3_model_sliding_order_from_page_locked_state(hip_device):
     4096 + 128256 x 4096), 8,030,261,248 params.  The global norm covers all 34
     segments.  Four of them are stepped in sliding order with the clip
     coefficient: lm_head, layers 31 and 30, embed.  Their fp32 master, m and v
-    are in page-locked host memory (one page-locked allocation per array and
-    segment) and stream through HBM in LayerAdam's default 16 Mi-element
+    are in page-locked host memory (one exact-size page-locked allocation per
+    array and segment) and stream through HBM in LayerAdam's default 16 Mi-element
     (64 MB) chunks; grads and bf16 copies are in HBM.  Each segment's results
     equal, bit for bit, the same step on HBM-resident copies, and windows at
     the start, across the first chunk boundary and at the end (in the short
@@ -116,12 +116,12 @@ def test_c3_model_sliding_order_from_page_locked_state(hip_device):
         p_d = torch.randn(n, generator=gen, device=dev) * 0.02
         m_d = torch.randn(n, generator=gen, device=dev) * 1e-5
         v_d = torch.rand(n, generator=gen, device=dev) * 1e-9
-        p_h = torch.empty(n, dtype=torch.float32, pin_memory=True)
+        p_h = _lib.page_locked_empty(n, torch.float32)
         p_h.copy_(p_d)
         assert adam.add_layer_params(pos[idx], [torch.nn.Parameter(p_h)]) == pos[idx]
         assert resident.add_layer_params(pos[idx], [torch.nn.Parameter(p_d)]) == pos[idx]
         m_h, v_h = adam.exp_avg_flat[pos[idx]], adam.exp_avg_sq_flat[pos[idx]]
-        assert _lib.is_page_locked(m_h) and _lib.is_page_locked(v_h) and p_h.is_pinned()
+        assert _lib.is_page_locked(m_h) and _lib.is_page_locked(v_h) and _lib.is_page_locked(p_h)
         m_h.copy_(m_d)
         v_h.copy_(v_d)
         resident.exp_avg_flat[pos[idx]].copy_(m_d)
