@@ -41,6 +41,7 @@
 #include <vector>
 
 #include "../../include/layer_adam.h"
+#include "hip_ptr.h"
 
 // Update workgroup size.  One wave per workgroup: in a one-shot grid a
 // finished wave is replaced at once instead of waiting for its siblings
@@ -802,20 +803,9 @@ uint64_t norm_workspace_bytes(uint64_t n) { return static_cast<uint64_t>(norm_gr
 int hip_rc(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); }
 
 // Whether the kernels may touch `ptr`: device (or managed / unified) memory.
-// A host address handed to a kernel faults the GPU: pageable memory reads as
-// unregistered here, page-locked memory as host memory, and both are refused
-// (host arrays go through la_pipeline_step).  The query is a lookup in the
-// runtime's allocation table, ~0.06 us on MI355X.
-bool device_accessible(const void* ptr)
-{
-    hipPointerAttribute_t a;
-    std::memset(&a, 0, sizeof(a));
-    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
-        (void)hipGetLastError();  // this query's own failure, not the caller's
-        return false;
-    }
-    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged || a.type == hipMemoryTypeUnified;
-}
+// A host address handed to a kernel faults the GPU: pageable and page-locked
+// host memory are both refused (host arrays go through la_pipeline_step).
+using la_ptr::device_accessible;
 
 // Launch `kernel` and return the status of this launch itself.  Arguments are
 // converted to the kernel's own parameter types and handed over by address;

@@ -49,6 +49,7 @@
 
 #include "../../include/layer_adam.h"
 #include "copy_pool.h"
+#include "hip_ptr.h"
 
 using la_host::CopyPool;
 using la_host::Piece;
@@ -128,28 +129,9 @@ int rc_of(hipError_t e) { return e == hipSuccess ? LA_OK : static_cast<int>(e); 
 
 // Host memory the copy engines can read and write directly: page-locked
 // (hipHostMalloc, torch pin_memory) or registered.  Anything else is pageable.
-bool page_locked(const void* ptr)
-{
-    hipPointerAttribute_t a;
-    std::memset(&a, 0, sizeof(a));
-    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
-        (void)hipGetLastError();  // a query of pageable memory must not leave an error behind
-        return false;
-    }
-    return a.type == hipMemoryTypeHost;
-}
-
+using la_ptr::page_locked;
 // Device (or managed / unified) memory, which the update may read and write in place.
-bool device_memory(const void* ptr)
-{
-    hipPointerAttribute_t a;
-    std::memset(&a, 0, sizeof(a));
-    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged || a.type == hipMemoryTypeUnified;
-}
+inline bool device_memory(const void* ptr) { return la_ptr::device_accessible(ptr); }
 
 // Host copies are split into pieces of at most this many bytes for the pool.
 constexpr uint64_t kPieceBytes = 1ull << 20;
