@@ -159,6 +159,31 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
     return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
 }
 
+// Two adjacent elements of a 16-bit store at once, low half first.  With
+// LA_HW_BF16 the bf16 pair is rounded by one v_cvt_pk_bf16_f32 (IEEE
+// round-to-nearest-even in the default mode, fp32 denormals kept).  Every NaN
+// is first replaced by 0x7FC00000, whose rounding is the reference's 0x7FC0;
+// the empty asm keeps that replaced value opaque, so the backend cannot treat
+// the replacement as a no-op (NaN payloads through a conversion are not
+// defined by the IR).
+#ifndef LA_HW_BF16
+#define LA_HW_BF16 1
+#endif
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi)
+{
+#if LA_HW_BF16
+    float c0 = (lo != lo) ? __uint_as_float(0x7fc00000u) : lo;
+    float c1 = (hi != hi) ? __uint_as_float(0x7fc00000u) : hi;
+    asm("" : "+v"(c0), "+v"(c1));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{c0, c1}, bf16x2_t));
+#else
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+#endif
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
 {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
@@ -234,8 +259,8 @@ template <typename Conv> struct Io16 {
     }
     __device__ __forceinline__ static void store4(void* base, uint64_t e, const float (&x)[kVec])
     {
-        const uint32_t lo = Conv::from_f32(x[0]) | (Conv::from_f32(x[1]) << 16);
-        const uint32_t hi = Conv::from_f32(x[2]) | (Conv::from_f32(x[3]) << 16);
+        const uint32_t lo = Conv::from_f32x2(x[0], x[1]);
+        const uint32_t hi = Conv::from_f32x2(x[2], x[3]);
         vstore<u32x2>(static_cast<uint16_t*>(base) + e, u32x2{lo, hi});
     }
     __device__ __forceinline__ static float load1(const void* base, uint64_t e)
@@ -251,10 +276,15 @@ template <typename Conv> struct Io16 {
 struct ConvBf16 {
     __device__ __forceinline__ static float to_f32(uint32_t h) { return bf16_bits_to_f32(h); }
     __device__ __forceinline__ static uint32_t from_f32(float f) { return f32_to_bf16_bits(f); }
+    __device__ __forceinline__ static uint32_t from_f32x2(float lo, float hi) { return f32x2_to_bf16x2_bits(lo, hi); }
 };
 struct ConvF16 {
     __device__ __forceinline__ static float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
     __device__ __forceinline__ static uint32_t from_f32(float f) { return f32_to_f16_bits(f); }
+    __device__ __forceinline__ static uint32_t from_f32x2(float lo, float hi)
+    {
+        return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+    }
 };
 template <> struct Io<bf16_t> : Io16<ConvBf16> {};
 template <> struct Io<f16_t> : Io16<ConvF16> {};
@@ -316,8 +346,8 @@ template <typename Conv> struct WaveIo16 {
     }
     __device__ __forceinline__ static void store4(rsrc_t r, uint32_t lane, const float (&x)[kVec])
     {
-        const uint32_t lo = Conv::from_f32(x[0]) | (Conv::from_f32(x[1]) << 16);
-        const uint32_t hi = Conv::from_f32(x[2]) | (Conv::from_f32(x[3]) << 16);
+        const uint32_t lo = Conv::from_f32x2(x[0], x[1]);
+        const uint32_t hi = Conv::from_f32x2(x[2], x[3]);
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, r, static_cast<int>(lane * 8), 0, kAuxSt);
     }
 };
@@ -500,7 +530,7 @@ template <typename Conv> struct WaveIo16x8 {
     {
         uint32_t w[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w[k] = Conv::from_f32(x[2 * k]) | (Conv::from_f32(x[2 * k + 1]) << 16);
+        for (int k = 0; k < 4; ++k) w[k] = Conv::from_f32x2(x[2 * k], x[2 * k + 1]);
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, static_cast<int>(lane * 16), 0,
                                                kAuxSt);
     }

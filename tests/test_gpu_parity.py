@@ -777,6 +777,44 @@ def test_fp16_store_rounding_of_every_fp32_bit_pattern(hip_device):
     torch.cuda.empty_cache()
 
 
+def test_bf16_master_store_rounding_of_every_fp32_bit_pattern(hip_device):
+    """The bf16 store of the master itself (not the copy stream), brute force
+    over all 2^32 fp32 bit patterns via the (bf16, f32, f32) triple, set up as
+    in the fp16 test above: the update computes p = fma(g, -1, +0), which is
+    -g exactly except that both zeros give +0, then stores p as bf16.  That
+    must equal the reference's bf16 store (simd.h:56-86) of the same value,
+    (u + 0x7FFF + ((u >> 16) & 1)) >> 16 with NaN -> 0x7FC0, for every input,
+    NaN grads included (they make p NaN).  Finite patterns with |g| >= 2^63
+    are left out: there g*g overflows, v turns NaN and so does p.  The
+    expected bits are integer arithmetic on the device."""
+    chunk = 1 << 28
+    hip = H.HipAdam(1.0, (0.0, 1.0), 0.0, 0.0, True)
+    p = torch.zeros(chunk, dtype=torch.bfloat16, device=hip_device)
+    m = torch.zeros(chunk, device=hip_device)
+    v = torch.ones(chunk, device=hip_device)
+    checked = 0
+    for c in range(16):
+        log(f"bf16 master rounding, patterns [{c * chunk:#x}, {(c + 1) * chunk:#x})")
+        u = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int64, device=hip_device)
+        g = u.to(torch.int32).view(torch.float32)
+        p.zero_()
+        m.zero_()
+        v.fill_(1.0)
+        hip.update(c + 1, 1.0, 0.0, 1.0, 0.0, 0.0, False, p, g, m, v)
+        mag = u & 0x7FFFFFFF
+        x = torch.where(mag == 0, torch.zeros_like(u), u ^ 0x80000000)          # 0 + -g
+        want = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16) & 0xFFFF
+        want = torch.where(mag > 0x7F800000, torch.full_like(want, 0x7FC0), want)
+        keep = (mag < 0x5F000000) | (mag > 0x7F800000)                             # |g| < 2^63, or NaN
+        got = p.view(torch.int16).to(torch.int64) & 0xFFFF
+        bad = int(((got != want) & keep).sum().item())
+        assert bad == 0, (c, bad)
+        checked += int(keep.sum().item())
+        del u, g, mag, x, want, keep, got
+    assert checked > (1 << 32) - (1 << 31)
+    torch.cuda.empty_cache()
+
+
 def test_sqrt_and_divide_over_fp32_bit_patterns(hip_device):
     """The kernel's correctly rounded sqrt and division over fp32 bit patterns
     of v via the (f32, f32, f32) triple: with lr 1, betas (0, 1), eps 0, no
