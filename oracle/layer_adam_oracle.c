@@ -287,7 +287,7 @@ static void sqnorm_block(int g_dtype, const void* g, uint64_t lo, uint64_t hi, d
         neumaier_add(&s, &c, x * x);  /* x * x is exact in binary64 for any binary32 x */
     }
     *s_out = s;
-    *c_out = c;
+    *c_out = isfinite(s) ? c : 0.0;  /* an inf term (or overflow) leaves inf - inf = NaN in c */
 }
 
 /* Sum of squares, compensated.  Large inputs are cut into a fixed number of
@@ -299,7 +299,7 @@ double orc_grad_sqnorm(int g_dtype, const void* g, uint64_t n)
     double s, c;
     if (n < (1u << 20)) {
         sqnorm_block(g_dtype, g, 0, n, &s, &c);
-        return s + c;
+        return s + c;  /* c is 0 when s is inf or NaN */
     }
     double bs[ORC_SQNORM_BLOCKS], bc[ORC_SQNORM_BLOCKS];
 #pragma omp parallel for schedule(static)
@@ -312,7 +312,7 @@ double orc_grad_sqnorm(int g_dtype, const void* g, uint64_t n)
         neumaier_add(&s, &c, bs[b]);
         neumaier_add(&s, &c, bc[b]);
     }
-    return s + c;
+    return isfinite(s) ? s + c : s;
 }
 
 /* torch.nn.utils.clip_grad_norm_: clip_coef = max_norm / (total_norm + 1e-6),

@@ -336,6 +336,28 @@ def test_sqnorm_is_exact_float64_sum(n):
     assert abs(O.grad_sqnorm(g.float().numpy().copy()) - exact) <= 1e-15 * exact
 
 
+@pytest.mark.parametrize("n", [5, 100001, 3_000_017])
+def test_sqnorm_of_non_finite_grads(n):
+    """An inf grad gives inf, as math.fsum and torch's norm do (the
+    compensation term must not turn inf - inf into NaN); a NaN grad gives NaN.
+    Both the short and the blocked parallel path.  Finite float32 grads cannot
+    overflow the float64 sum: each square is at most 1.2e77."""
+    x = np.full(n, 1e-3, np.float32)
+    for pos in (0, n // 2, n - 1):
+        y = x.copy()
+        y[pos] = np.inf
+        assert O.grad_sqnorm(y) == math.inf
+        assert O.grad_sqnorm(y.astype(np.float16).view(np.uint16), "f16") == math.inf
+        y[pos] = -np.inf
+        assert O.grad_sqnorm(y) == math.inf
+        y[pos] = np.nan
+        assert math.isnan(O.grad_sqnorm(y))
+    big = np.full(n, np.finfo(np.float32).max, np.float32)
+    exact = math.fsum([float(big[0]) ** 2] * n)
+    assert abs(O.grad_sqnorm(big) - exact) <= 1e-15 * exact
+    assert math.fsum([math.inf, 1.0]) == math.inf
+
+
 def test_clip_coef_matches_torch_clip_grad_norm():
     rng = np.random.default_rng(6)
     for scale, max_norm in ((1e-3, 1.0), (1e-1, 1.0), (1e-5, 1.0), (1.0, 0.5)):
