@@ -121,13 +121,17 @@
 // 0.917 ms.  Wave priority and the write-through stores still add 1-3 % on
 // top of the cap.
 // The best cap differs by triple: bytes per element and conversion work
-// differ, and so do the waves needed to hide them.  At the C2 shape, same box
-// (ms per launch at 16 / 13 / 12 / 10 waves per CU or uncapped):
-// (bf16, bf16, bf16) best at 20 waves (8 KiB, 0.580 against 0.594 uncapped,
-// 0.664 at 12); (f16, f16, f16) and (f16, f16, f32) best at 16 (10 KiB: 0.552
-// and 0.805, against 0.577 and 0.836 uncapped); (f32, f32, f32) best at 10
-// (16 KiB: 0.978 against 0.996 at 12); the others at 12.  LA_UPDATE_LDS_BYTES,
-// when defined, overrides the table for every triple.
+// differ, and so do the waves needed to hide them.  At the C2 shape, one box,
+// reserved 10 / 12 / 13 / 14 / 15 / 16 KiB, two runs each (ms per launch):
+// (f32, f32, f32) 0.996 / 0.979 / 0.977 / 0.975 / 0.975 / 0.986, kept 14 KiB;
+// (f16, f16, f32) 0.812 / 0.789 / 0.786 / 0.802 / 0.803 / 0.835 and every
+// other triple of this layout best at 13 KiB (12 waves).  A previous build,
+// with the wave index in vector registers, was best at 16 KiB for
+// (f32, f32, f32) and at 10 KiB for (f16, f16, f32).  The all-16-bit triples
+// normally run la_adamw16_kernel (own cap below); with LA_WIDE16=0 they take
+// this kernel, best there at 8 KiB (bf16) and 10 KiB (f16) on the previous
+// build.  LA_UPDATE_LDS_BYTES, when defined, overrides the table for every
+// triple.
 #ifdef LA_UPDATE_LDS_BYTES
 #define LA_UPDATE_LDS_OVERRIDE 1
 #else
@@ -861,8 +865,8 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t update_lds_b
 {
     if (LA_UPDATE_LDS_OVERRIDE) return LA_UPDATE_LDS_BYTES;
     if (std::is_same<TP, bf16_t>::value && std::is_same<TS, bf16_t>::value) return 8192;       // (bf16, bf16, bf16)
-    if (std::is_same<TP, f16_t>::value && std::is_same<TG, f16_t>::value) return 10240;       // (f16, f16, f16 / f32)
-    if (std::is_same<TP, float>::value && std::is_same<TG, float>::value) return 16384;       // (f32, f32, f32)
+    if (std::is_same<TP, f16_t>::value && std::is_same<TS, f16_t>::value) return 10240;       // (f16, f16, f16)
+    if (std::is_same<TP, float>::value && std::is_same<TG, float>::value) return 14336;       // (f32, f32, f32)
     return LA_UPDATE_LDS_BYTES;
 }
 
