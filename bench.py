@@ -892,8 +892,9 @@ def main():
                     help="seconds of CPU-baseline timing (0 disables it)")
     ap.add_argument("--no-clip", action="store_true", help="time the update alone (no norm pass)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
-                    help="before timing, run one torch fp32 copy_ of this many MiB: a plain copy "
-                         "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
+                    help="before timing, run one torch fp32 elementwise multiply over this many MiB "
+                         "(reads and writes that many): a kernel of known traffic, to check rocprofv3 "
+                         "read/write counters against")
     ap.add_argument("--pageable", action="store_true",
                     help="with --streamed: host state in pageable instead of pinned memory")
     ap.add_argument("--host-threads", type=int, default=0,
