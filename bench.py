@@ -733,8 +733,10 @@ def step_api(args):
     step_with_grad_views (bf16 grad views, :362-428) -- both one
     la_adam_update_multi call per layer -- against one adam_update call per
     tensor (the reference's loop) and against step_chunk on the same layer
-    held flat.  C1 = a GPT-2-small block (12 tensors), C2 = a Llama-3.1-8B
-    layer (9 tensors)."""
+    held flat; and the grad norm with clip over the same grads, through
+    clip_grad_norm (la_grad_norm_multi: two launches for up to 32 tensors)
+    against la_grad_sqnorm per tensor.  C1 = a GPT-2-small block (12 tensors),
+    C2 = a Llama-3.1-8B layer (9 tensors)."""
     import torch
 
     from slideformer_amd import LayerAdam
@@ -763,11 +765,33 @@ def step_api(args):
             adam.adam_update(group['step'], group['lr'], 0.9, 0.999, group['eps'], group['weight_decay'],
                              group['bias_correction'], p.data, p.grad.data, st['exp_avg'], st['exp_avg_sq'])
 
+    from slideformer_amd import _lib
+    vgrads = list(views.values())
+    ws = torch.empty(max(1, adam.lib.la_grad_sqnorm_workspace(1 << 62) // 8), dtype=torch.float64, device=dev)
+    sq = torch.empty(1, dtype=torch.float64, device=dev)
+    cf = torch.empty(1, device=dev)
+
+    def norm_per_buffer():
+        # the grad norm one buffer at a time: la_grad_sqnorm per tensor, the
+        # last one la_grad_norm_clip (two launches per tensor)
+        h = stream.cuda_stream
+        for i, g in enumerate(vgrads):
+            if i < len(vgrads) - 1:
+                rc = adam.lib.la_grad_sqnorm(_lib.LA_BF16, g.data_ptr(), g.numel(), ws.data_ptr(), ws.numel() * 8,
+                                             sq.data_ptr(), int(i > 0), h)
+            else:
+                rc = adam.lib.la_grad_norm_clip(_lib.LA_BF16, g.data_ptr(), g.numel(), ws.data_ptr(),
+                                                ws.numel() * 8, sq.data_ptr(), int(i > 0), 1.0, cf.data_ptr(),
+                                                None, h)
+            _lib.check(rc, "norm")
+
     cases = {
         "step(layer), fp32 grads": lambda: adam.step(0),
         "step_with_grad_views, bf16 grads": lambda: adam.step_with_grad_views(0, views),
         "one adam_update per tensor, fp32 grads": per_call,
         "step_chunk on the flat layer, bf16 grads": lambda: adam.step_chunk(*flat, group),
+        "clip_grad_norm over the bf16 grad views (la_grad_norm_multi)": lambda: adam.clip_grad_norm(vgrads, 1.0),
+        "grad norm one buffer at a time (la_grad_sqnorm per tensor)": norm_per_buffer,
     }
     stream = torch.cuda.current_stream(dev)
     res = {}

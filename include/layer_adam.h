@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 8
+#define LA_ABI_VERSION 9
 
 #define LA_OK 0
 #define LA_EINVAL (-22)
@@ -159,6 +159,32 @@ int la_grad_sqnorm(int g_dtype, const void* g, uint64_t n, void* workspace,
 int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace,
                       uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm,
                       float* coef, float* norm_out, la_stream_t stream);
+
+/*
+ * The grad norm over several buffers of one element type in two launches
+ * (one stage-1 launch that reads every buffer, one fold), where
+ * la_grad_sqnorm would take two per buffer: for grads held per tensor, as
+ * step(layer) and step_with_grad_views take them (layer_adam.py:299-327,
+ * 391-422).  No counterpart in the reference, which has no clipping.
+ * bufs[0..count) with 1 <= count <= LA_NORM_MULTI_MAX; a buffer may be empty
+ * (g may then be NULL).  The sum of squares of all of them goes into *sqnorm,
+ * added to the old value when accumulate != 0; with coef != NULL the fold
+ * also writes the clip coefficient (and *norm_out when not NULL), as
+ * la_grad_norm_clip does.  `workspace`: at least la_grad_sqnorm_workspace(N)
+ * bytes for N the buffers' total element count.  Deterministic for given
+ * sizes and pointer alignments; with one buffer the result is bit-identical
+ * to la_grad_sqnorm's / la_grad_norm_clip's.  Every pointer is checked before
+ * the first launch.
+ */
+#define LA_NORM_MULTI_MAX 32
+typedef struct {
+    const void* g;  /* grads, g_dtype */
+    uint64_t n;
+} la_grad_buffer_t;
+
+int la_grad_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, void* workspace,
+                       uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm,
+                       float* coef, float* norm_out, la_stream_t stream);
 
 /*
  * la_grad_norm_clip without a workspace: for callers that cannot allocate

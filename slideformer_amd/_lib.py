@@ -34,6 +34,8 @@ LA_ON_HOST_ALL = 31
 
 # la_disk_create_ex flags
 LA_DISK_DIRECT = 1
+# buffers per la_grad_norm_multi call
+LA_NORM_MULTI_MAX = 32
 
 # every exported symbol of include/layer_adam.h
 EXPORTED = (
@@ -48,6 +50,7 @@ EXPORTED = (
     "la_grad_sqnorm_workspace",
     "la_grad_sqnorm",
     "la_grad_norm_clip",
+    "la_grad_norm_multi",
     "la_grad_norm_clip_noalloc",
     "la_clip_coef",
     "la_pipeline_workspace_bytes",
@@ -91,6 +94,15 @@ class LaSegment(ctypes.Structure):
         ("m", ctypes.c_void_p),
         ("v", ctypes.c_void_p),
         ("p_bf16_out", ctypes.c_void_p),
+        ("n", ctypes.c_uint64),
+    ]
+
+
+class LaGradBuffer(ctypes.Structure):
+    """Mirror of ``la_grad_buffer_t``."""
+
+    _fields_ = [
+        ("g", ctypes.c_void_p),
         ("n", ctypes.c_uint64),
     ]
 
@@ -146,6 +158,8 @@ def _declare(L):
     L.la_grad_sqnorm.restype = i
     L.la_grad_norm_clip.argtypes = [i, P, u64, P, u64, P, i, f, P, P, P]
     L.la_grad_norm_clip.restype = i
+    L.la_grad_norm_multi.argtypes = [i, ctypes.POINTER(LaGradBuffer), i, P, u64, P, i, f, P, P, P]
+    L.la_grad_norm_multi.restype = i
     L.la_grad_norm_clip_noalloc.argtypes = [i, P, u64, P, i, f, P, P, P]
     L.la_grad_norm_clip_noalloc.restype = i
     L.la_clip_coef.argtypes = [P, f, P, P, P]

@@ -717,17 +717,18 @@ struct NormArgs {
     float* norm_out;      // may be null
 };
 
+// One buffer's share of stage 1 for thread `tid` of `stride`: its aligned
+// groups of 4, walked from the top of the buffer down, then its scalar head
+// and remainder, added into `acc` in a fixed order.
 template <typename TG, bool NT>
-__global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
+__device__ __forceinline__ void sqnorm_buffer(const void* g, uint64_t n, uint64_t head, uint64_t nvec, uint64_t tid,
+                                              uint64_t stride, double& acc)
 {
-    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_NORM_BLOCK + threadIdx.x;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_NORM_BLOCK;
     // aligned group i of the walk -> group index in the buffer
-    auto group = [&a](uint64_t i) { return LA_NORM_DESCENDING ? a.nvec - 1 - i : i; };
-    auto load = [&a](uint64_t gidx, float (&x)[kVec]) { Io<TG>::template load4<NT>(a.g, a.head + gidx * kVec, x); };
-    double acc = 0.0;
+    auto group = [nvec](uint64_t i) { return LA_NORM_DESCENDING ? nvec - 1 - i : i; };
+    auto load = [g, head](uint64_t gidx, float (&x)[kVec]) { Io<TG>::template load4<NT>(g, head + gidx * kVec, x); };
     uint64_t gi = tid;
-    for (; gi + (LA_NORM_UNROLL - 1) * stride < a.nvec; gi += LA_NORM_UNROLL * stride) {
+    for (; gi + (LA_NORM_UNROLL - 1) * stride < nvec; gi += LA_NORM_UNROLL * stride) {
         float x[LA_NORM_UNROLL][kVec];
 #pragma unroll
         for (int u = 0; u < LA_NORM_UNROLL; ++u) load(group(gi + u * stride), x[u]);
@@ -739,7 +740,7 @@ __global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
                 acc = __builtin_fma(d, d, acc);
             }
     }
-    for (; gi < a.nvec; gi += stride) {
+    for (; gi < nvec; gi += stride) {
         float x[kVec];
         load(group(gi), x);
 #pragma unroll
@@ -748,14 +749,44 @@ __global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
             acc = __builtin_fma(d, d, acc);
         }
     }
-    const uint64_t vec_end = a.head + a.nvec * kVec;
-    const uint64_t nscalar = a.head + (a.n - vec_end);
+    const uint64_t vec_end = head + nvec * kVec;
+    const uint64_t nscalar = head + (n - vec_end);
     for (uint64_t s = tid; s < nscalar; s += stride) {
-        const uint64_t e = s < a.head ? s : vec_end + (s - a.head);
-        const double d = static_cast<double>(Io<TG>::load1(a.g, e));
+        const uint64_t e = s < head ? s : vec_end + (s - head);
+        const double d = static_cast<double>(Io<TG>::load1(g, e));
         acc = __builtin_fma(d, d, acc);
     }
+}
 
+template <typename TG, bool NT>
+__global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_kernel(NormArgs a)
+{
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_NORM_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_NORM_BLOCK;
+    double acc = 0.0;
+    sqnorm_buffer<TG, NT>(a.g, a.n, a.head, a.nvec, tid, stride, acc);
+    const double t = block_sum_f64(acc);
+    if (threadIdx.x == 0) a.partials[blockIdx.x] = t;
+}
+
+// Stage 1 over up to LA_NORM_MULTI_MAX buffers of one element type in one
+// launch: every thread takes its share of each buffer in turn, so a buffer of
+// any size is spread over the whole grid, and the partials hold the sum over
+// all of them.
+struct NormMultiArgs {
+    const void* g[LA_NORM_MULTI_MAX];
+    uint64_t n[LA_NORM_MULTI_MAX], head[LA_NORM_MULTI_MAX], nvec[LA_NORM_MULTI_MAX];
+    int32_t count;
+    double* partials;
+};
+
+template <typename TG, bool NT>
+__global__ __launch_bounds__(LA_NORM_BLOCK) void la_sqnorm_multi_kernel(NormMultiArgs a)
+{
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * LA_NORM_BLOCK + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * LA_NORM_BLOCK;
+    double acc = 0.0;
+    for (int b = 0; b < a.count; ++b) sqnorm_buffer<TG, NT>(a.g[b], a.n[b], a.head[b], a.nvec[b], tid, stride, acc);
     const double t = block_sum_f64(acc);
     if (threadIdx.x == 0) a.partials[blockIdx.x] = t;
 }
@@ -1134,6 +1165,77 @@ int launch_norm(int g_dtype, const void* g, uint64_t n, void* workspace, uint64_
     return launch(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);
 }
 
+int launch_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, void* workspace,
+                      uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm, float* coef,
+                      float* norm_out, hipStream_t st)
+{
+    if (!dt_valid(g_dtype)) return LA_EDTYPE;
+    if (!bufs || count < 1 || count > LA_NORM_MULTI_MAX || !sqnorm || !workspace) return LA_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(sqnorm) & 7u) || (reinterpret_cast<uintptr_t>(workspace) & 7u)) return LA_EINVAL;
+    if (coef && (reinterpret_cast<uintptr_t>(coef) & 3u)) return LA_EINVAL;
+    if (norm_out && (reinterpret_cast<uintptr_t>(norm_out) & 3u)) return LA_EINVAL;
+    const int gb = elem_bytes(g_dtype);
+    uint64_t total = 0;
+    for (int b = 0; b < count; ++b) {
+        const la_grad_buffer_t& q = bufs[b];
+        if (q.n > 0 && (!q.g || reinterpret_cast<uintptr_t>(q.g) % static_cast<uintptr_t>(gb))) return LA_EINVAL;
+        if (q.n > UINT64_MAX - total) return LA_EINVAL;
+        total += q.n;
+    }
+    if (workspace_bytes < norm_workspace_bytes(total)) return LA_EINVAL;
+    if (!device_accessible(workspace) || !device_accessible(sqnorm) || (coef && !device_accessible(coef)) ||
+        (norm_out && !device_accessible(norm_out)))
+        return LA_EFAULT;
+    for (int b = 0; b < count; ++b)
+        if (bufs[b].n > 0 && !device_accessible(bufs[b].g)) return LA_EFAULT;
+
+    NormMultiArgs m;
+    m.count = count;
+    m.partials = static_cast<double*>(workspace);
+    for (int b = 0; b < LA_NORM_MULTI_MAX; ++b) {
+        m.g[b] = nullptr;
+        m.n[b] = m.head[b] = m.nvec[b] = 0;
+    }
+    for (int b = 0; b < count; ++b) {
+        const uint64_t n = bufs[b].n;
+        m.g[b] = bufs[b].g;
+        m.n[b] = n;
+        const uintptr_t addr = reinterpret_cast<uintptr_t>(bufs[b].g);
+        const int h = n > 0 ? common_head(&addr, &gb, 1) : -1;
+        if (h >= 0 && static_cast<uint64_t>(h) < n) {
+            m.head[b] = static_cast<uint64_t>(h);
+            m.nvec[b] = (n - m.head[b]) / kVec;
+        }
+    }
+    const uint32_t grid = norm_grid(total);
+    // plain loads for the read that produces the coefficient, nontemporal otherwise
+    const bool nt = !(coef && LA_NORM_CLIP_PLAIN);
+    int rc;
+    switch (g_dtype) {
+    case LA_F32:
+        rc = launch(nt ? la_sqnorm_multi_kernel<float, true> : la_sqnorm_multi_kernel<float, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, m);
+        break;
+    case LA_BF16:
+        rc = launch(nt ? la_sqnorm_multi_kernel<bf16_t, true> : la_sqnorm_multi_kernel<bf16_t, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, m);
+        break;
+    default:
+        rc = launch(nt ? la_sqnorm_multi_kernel<f16_t, true> : la_sqnorm_multi_kernel<f16_t, false>, dim3(grid),
+                    dim3(LA_NORM_BLOCK), 0, st, m);
+        break;
+    }
+    if (rc != LA_OK) return rc;
+    NormArgs a{};
+    a.partials = m.partials;
+    a.sqnorm = sqnorm;
+    a.accumulate = accumulate ? 1 : 0;
+    a.max_norm = max_norm;
+    a.coef = coef;
+    a.norm_out = norm_out;
+    return launch(la_sqnorm_finish, dim3(1), dim3(LA_NORM_BLOCK), 0, st, a, grid);
+}
+
 }  // namespace
 
 // Fixed device scratch of la_grad_norm_clip_noalloc: the grad norm's stage-1
@@ -1359,6 +1461,14 @@ int la_grad_norm_clip(int g_dtype, const void* g, uint64_t n, void* workspace, u
     if (!coef) return LA_EINVAL;
     return launch_norm(g_dtype, g, n, workspace, workspace_bytes, sqnorm, accumulate, max_norm, coef, norm_out,
                        static_cast<hipStream_t>(stream));
+}
+
+int la_grad_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, void* workspace,
+                       uint64_t workspace_bytes, double* sqnorm, int accumulate, float max_norm, float* coef,
+                       float* norm_out, la_stream_t stream)
+{
+    return launch_norm_multi(g_dtype, bufs, count, workspace, workspace_bytes, sqnorm, accumulate, max_norm, coef,
+                             norm_out, static_cast<hipStream_t>(stream));
 }
 
 int la_grad_norm_clip_noalloc(int g_dtype, const void* g, uint64_t n, double* sqnorm, int accumulate,

@@ -270,9 +270,15 @@ def _torch_stream(stream, device):
     return torch.cuda.ExternalStream(int(stream), device=device)
 
 
+_norm_elems = None
+
+
 def _norm_workspace_elems(lib) -> int:
     """float64 partials for any buffer size: stage 1 never uses more workgroups than this."""
-    return max(1, lib.la_grad_sqnorm_workspace(1 << 62) // 8)
+    global _norm_elems
+    if _norm_elems is None:
+        _norm_elems = max(1, lib.la_grad_sqnorm_workspace(1 << 62) // 8)
+    return _norm_elems
 
 
 class LayerAdam:
@@ -765,8 +771,10 @@ class LayerAdam:
 
         Returns ``(coef, norm)``: fp32 device scalars with
         ``coef = min(1, max_norm / (norm + 1e-6))`` (torch.nn.utils.clip_grad_norm_
-        convention).  Pass ``coef`` as ``clip_coef=`` to ``step_chunk``.
-        Nothing is synchronised with the host.
+        convention), one-element views of this call's scratch.  Pass ``coef`` as
+        ``clip_coef=`` to ``step_chunk``.  The grads go to the library in runs of
+        one dtype, up to 32 tensors per la_grad_norm_multi call (two launches
+        each).  Nothing is synchronised with the host.
         """
         grads = [g for g in grads if g is not None]
         if not grads:
@@ -781,28 +789,42 @@ class LayerAdam:
                 raise RuntimeError("grads must be contiguous")
             if g.dtype not in _DTYPE_CODE:
                 raise RuntimeError(f"unsupported grad dtype {g.dtype}")
-        with torch.cuda.device(device):
+        nwork = _norm_workspace_elems(self.lib)
+        with _on_device(device):
             s = _torch_stream(stream, device)
             handle = s.cuda_stream
-            # scratch of this call only, allocated on the stream it is used on:
-            # calls on different streams share nothing
-            with torch.cuda.stream(s):
-                coef = torch.empty(1, dtype=torch.float32, device=device)
-                norm = torch.empty(1, dtype=torch.float32, device=device)
-                sqnorm = torch.empty(1, dtype=torch.float64, device=device)
-                work = torch.empty(_norm_workspace_elems(self.lib), dtype=torch.float64, device=device)
-            last = len(grads) - 1
-            for i, g in enumerate(grads):
-                # the first buffer overwrites sqnorm, later ones add to it
-                if i < last:
-                    rc = self.lib.la_grad_sqnorm(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
-                                                 work.numel() * 8, _ptr(sqnorm), int(i > 0), handle)
+            # scratch of this call only, one allocation on the stream it is used
+            # on, so calls on different streams share nothing: the partials,
+            # the float64 sum, then coef and norm as two fp32 in one more slot
+            if stream is None:
+                buf = torch.empty(nwork + 2, dtype=torch.float64, device=device)
+            else:
+                with torch.cuda.stream(s):
+                    buf = torch.empty(nwork + 2, dtype=torch.float64, device=device)
+            base = buf.data_ptr()
+            work, sqnorm, cn = base, base + nwork * 8, base + (nwork + 1) * 8
+            pair = buf[nwork + 1:].view(torch.float32)
+            coef, norm = pair[0:1], pair[1:2]
+            # runs of one dtype, at most LA_NORM_MULTI_MAX buffers each, one
+            # la_grad_norm_multi call per run (two launches): the first run
+            # overwrites the sum, later ones add to it, the last one also writes
+            # the coefficient
+            runs = []
+            for g in grads:
+                if runs and runs[-1][0].dtype == g.dtype and len(runs[-1]) < _lib.LA_NORM_MULTI_MAX:
+                    runs[-1].append(g)
                 else:
-                    # the last buffer also writes the coefficient, in the same launch
-                    rc = self.lib.la_grad_norm_clip(_DTYPE_CODE[g.dtype], _ptr(g), g.numel(), _ptr(work),
-                                                    work.numel() * 8, _ptr(sqnorm), int(i > 0),
-                                                    float(max_norm), _ptr(coef), _ptr(norm), handle)
-                _lib.check(rc, "la_grad_sqnorm")
+                    runs.append([g])
+            for i, run in enumerate(runs):
+                flat = []
+                for g in run:
+                    flat += (g.data_ptr(), g.numel())
+                bufs = ctypes.cast((ctypes.c_uint64 * len(flat))(*flat), ctypes.POINTER(_lib.LaGradBuffer))
+                last = i == len(runs) - 1
+                rc = self.lib.la_grad_norm_multi(_DTYPE_CODE[run[0].dtype], bufs, len(run), work, nwork * 8, sqnorm,
+                                                 int(i > 0), float(max_norm), cn if last else None,
+                                                 cn + 4 if last else None, handle)
+                _lib.check(rc, "la_grad_norm_multi")
         return coef, norm
 
     def grad_norm_begin(self, device=None) -> "GradNormAccumulator":

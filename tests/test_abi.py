@@ -36,10 +36,11 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
-    assert L.la_abi_version() == version == 8
+    assert L.la_abi_version() == version == 9
     header = _read(HEADER)
     for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_EFAULT", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
-                 "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL"):
+                 "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL",
+                 "LA_NORM_MULTI_MAX"):
         value = int(re.search(rf"#define {name} \(?(-?\d+)u?\)?", header).group(1))
         assert getattr(_lib, name) == value, name
 
@@ -128,6 +129,26 @@ def test_error_codes_without_launch():
     assert L.la_adamw_step(ctypes.byref(sc), 0, hp, 0, hp, 0, hp, hp, 8, None, None, None) == _lib.LA_EFAULT
     assert L.la_grad_sqnorm(0, hp, 8, hp, 64, hp, 0, None) == _lib.LA_EFAULT
     assert L.la_clip_coef(hp, 1.0, hp, None, None) == _lib.LA_EFAULT
+    # the multi-buffer norm: buffer count, null / misaligned buffers, workspace size,
+    # host memory; every check comes before the first launch
+    bufs = (_lib.LaGradBuffer * 33)()
+    for b in bufs:
+        b.g, b.n = hp, 8
+    multi = L.la_grad_norm_multi
+    assert multi(1, None, 1, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    assert multi(1, bufs, 0, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    assert multi(1, bufs, _lib.LA_NORM_MULTI_MAX + 1, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    assert multi(7, bufs, 1, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EDTYPE
+    assert multi(1, bufs, 2, hp, 64, None, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    assert multi(1, bufs, 2, hp + 4, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL    # workspace alignment
+    assert multi(1, bufs, 2, hp, 0, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL         # workspace too small
+    bufs[1].g = hp + 1                                                                    # odd for 2-byte grads
+    assert multi(1, bufs, 2, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    bufs[1].g, bufs[1].n = None, 5
+    assert multi(1, bufs, 2, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EINVAL
+    bufs[1].n = 0                                                                         # empty: g may be NULL
+    assert multi(1, bufs, 2, hp, 64, hp, 0, 1.0, hp, None, None) == _lib.LA_EFAULT
+    assert multi(1, bufs, _lib.LA_NORM_MULTI_MAX, hp, 64, hp, 1, 0.0, None, None, None) == _lib.LA_EFAULT
     assert b"device memory" in L.la_strerror(_lib.LA_EFAULT)
     assert b"dtype" in L.la_strerror(_lib.LA_EDTYPE)
     assert b"memory" in L.la_strerror(_lib.LA_ENOMEM)

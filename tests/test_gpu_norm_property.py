@@ -12,7 +12,9 @@ exact one (the checker's compensated float64 sum, itself pinned to math.fsum
 by the CPU tests); the coefficient and the norm must be bit-identical to the
 checker's clip of the sum the device produced (the torch clip_grad_norm_
 formula); la_clip_coef on that sum and the no-workspace variant run over the
-same sequence must give the same bits.  Examples are drawn from a fixed seed."""
+same sequence must give the same bits.  The same buffers then go through
+la_grad_norm_multi in runs of one dtype, to the same bar (with bit equality
+when every run holds one buffer).  Examples are drawn from a fixed seed."""
 from __future__ import annotations
 
 import math
@@ -102,3 +104,102 @@ def test_accumulated_norm_and_clip_equal_checker(c, hip_device):
     assert coef2.item() == coef.item() and norm2.item() == norm.item()
     # the no-workspace sequence: the same partial order, so the same bits
     assert sq_na.item() == got and coef_na.item() == coef.item() and norm_na.item() == norm.item()
+
+    # the multi-buffer norm over runs of one dtype (as LayerAdam.clip_grad_norm
+    # groups them): its own summation order, so within 1e-12 of the exact sum,
+    # and the clip of its sum bit-exact; a run of one buffer is the single-buffer
+    # computation, so with every run of length one the bits equal the sequence above
+    runs = []
+    for b, g in zip(c["buffers"], grads):
+        if runs and runs[-1][0][0] == b["kind"] and len(runs[-1]) < _lib.LA_NORM_MULTI_MAX:
+            runs[-1].append((b["kind"], g))
+        else:
+            runs.append([(b["kind"], g)])
+    sq_m = torch.full((1,), 777.0, dtype=torch.float64, device=hip_device)
+    coef_m = torch.zeros(1, device=hip_device)
+    norm_m = torch.zeros(1, device=hip_device)
+    for i, run in enumerate(runs):
+        bufs = (_lib.LaGradBuffer * len(run))()
+        for q, (_, g) in zip(bufs, run):
+            q.g, q.n = g.data_ptr(), g.numel()
+        last = i == len(runs) - 1
+        rc = L.la_grad_norm_multi(H.CODE[run[0][0]], bufs, len(run), ws.data_ptr(), ws.numel() * 8, sq_m.data_ptr(),
+                                  int(i > 0), c["max_norm"], coef_m.data_ptr() if last else None,
+                                  norm_m.data_ptr() if last else None, st_)
+        assert rc == 0, L.la_strerror(rc)
+    torch.cuda.synchronize()
+    got_m = float(sq_m.item())
+    if math.isinf(exact):
+        assert got_m == exact
+    else:
+        assert abs(got_m - exact) <= 1e-12 * exact, (got_m, exact)
+    c_ref, n_ref = O.clip_coef(got_m, c["max_norm"])
+    assert coef_m.cpu().numpy()[0] == np.float32(c_ref) and norm_m.cpu().numpy()[0] == np.float32(n_ref)
+    if all(len(run) == 1 for run in runs):
+        assert got_m == got and coef_m.item() == coef.item() and norm_m.item() == norm.item()
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("count", [1, 2, 31, 32])
+def test_multi_norm_of_many_small_buffers(kind, count, hip_device):
+    """Up to LA_NORM_MULTI_MAX buffers in one call: sizes 0-5000 (most far below
+    one workgroup's share), each at an element offset 0-7 of its allocation.
+    The sum is within 1e-12 of the exact one, the clip bit-exact to the
+    checker's clip of that sum; a second identical call gives the same bits."""
+    print(f"multi norm: {kind} x {count}", flush=True)
+    L = _lib.load()
+    rng = np.random.default_rng(count * 7 + len(kind))
+    bufs = (_lib.LaGradBuffer * count)()
+    keep, exact = [], 0.0
+    for q in bufs:
+        n, off = int(rng.integers(0, 5000)), int(rng.integers(0, 8))
+        bits = _bits(rng.normal(0, 1e-2, n + off), kind)
+        view = bits.view(np.float32) if kind == "f32" else bits
+        exact += O.grad_sqnorm(view[off:], KIND16[kind])
+        g = H.to_dev_bits(bits, kind, hip_device)[off:]
+        keep.append(g)
+        q.g, q.n = g.data_ptr(), g.numel()
+    total = sum(g.numel() for g in keep)
+    ws = torch.zeros(max(1, L.la_grad_sqnorm_workspace(total) // 8), dtype=torch.float64, device=hip_device)
+    out = []
+    for _ in range(2):
+        sq = torch.zeros(1, dtype=torch.float64, device=hip_device)
+        coef = torch.zeros(1, device=hip_device)
+        norm = torch.zeros(1, device=hip_device)
+        rc = L.la_grad_norm_multi(H.CODE[kind], bufs, count, ws.data_ptr(), ws.numel() * 8, sq.data_ptr(), 0, 1.0,
+                                  coef.data_ptr(), norm.data_ptr(), torch.cuda.current_stream(hip_device).cuda_stream)
+        assert rc == 0, L.la_strerror(rc)
+        torch.cuda.synchronize()
+        out.append((sq.item(), coef.item(), norm.item()))
+    got = out[0][0]
+    assert abs(got - exact) <= 1e-12 * exact
+    c_ref, n_ref = O.clip_coef(got, 1.0)
+    assert out[0][1] == np.float32(c_ref) and out[0][2] == np.float32(n_ref)
+    assert out[0] == out[1]
+
+
+def test_clip_grad_norm_over_many_tensors_of_mixed_dtype(hip_device):
+    """LayerAdam.clip_grad_norm over 75 grad tensors (more than two
+    la_grad_norm_multi calls' worth, three dtypes, empty ones among them):
+    the norm is the exact float64 norm rounded to fp32 (within one ulp, since
+    the device's float64 sum may differ from the exact one in its last bits)
+    and the coefficient follows from it as torch's clip_grad_norm_ computes."""
+    from slideformer_amd import LayerAdam
+
+    rng = np.random.default_rng(75)
+    kinds = ["bf16"] * 40 + ["f32"] * 20 + ["bf16"] * 5 + ["f16"] * 10
+    grads, exact = [], 0.0
+    for k, kind in enumerate(kinds):
+        n = 0 if k % 17 == 3 else int(rng.integers(1, 20_000))
+        bits = _bits(rng.normal(0, 3e-3, n), kind)
+        view = bits.view(np.float32) if kind == "f32" else bits
+        exact += O.grad_sqnorm(view, KIND16[kind])
+        grads.append(H.to_dev_bits(bits, kind, hip_device))
+    adam = LayerAdam()
+    coef, norm = adam.clip_grad_norm(grads, 0.05)
+    torch.cuda.synchronize()
+    want = np.float32(math.sqrt(exact))
+    assert abs(float(norm.item()) - float(want)) <= float(np.spacing(want))
+    c_ref, n_ref = O.clip_coef(float(norm.item()) ** 2, 0.05)
+    assert abs(coef.item() - c_ref) <= 2 * float(np.spacing(np.float32(c_ref)))
+    assert 0.0 < coef.item() < 1.0
