@@ -281,6 +281,40 @@ def _norm_workspace_elems(lib) -> int:
     return _norm_elems
 
 
+def _norm_runs(lib, grads, work, nwork, sqnorm, accumulate, max_norm, cn, handle):
+    """The sum of squares of ``grads`` into the float64 at ``sqnorm`` (added to
+    it when ``accumulate``): runs of one dtype, at most LA_NORM_MULTI_MAX
+    buffers each, one la_grad_norm_multi call (two launches) per run, later
+    runs adding to the earlier ones.  With ``cn`` (address of two fp32: coef,
+    norm) the last call also writes the clip coefficient."""
+    runs = []
+    for g in grads:
+        if runs and runs[-1][0].dtype == g.dtype and len(runs[-1]) < _lib.LA_NORM_MULTI_MAX:
+            runs[-1].append(g)
+        else:
+            runs.append([g])
+    for i, run in enumerate(runs):
+        flat = []
+        for g in run:
+            flat += (g.data_ptr(), g.numel())
+        bufs = ctypes.cast((ctypes.c_uint64 * len(flat))(*flat), ctypes.POINTER(_lib.LaGradBuffer))
+        last = cn is not None and i == len(runs) - 1
+        rc = lib.la_grad_norm_multi(_DTYPE_CODE[run[0].dtype], bufs, len(run), work, nwork * 8, sqnorm,
+                                    int(accumulate or i > 0), max_norm, cn if last else None,
+                                    cn + 4 if last else None, handle)
+        _lib.check(rc, "la_grad_norm_multi")
+
+
+def _check_grads(grads, device):
+    for g in grads:
+        if g.device != device:
+            raise RuntimeError(f"grad on {g.device}, expected {device}: all grads must be on one device")
+        if not g.is_contiguous():
+            raise RuntimeError("grads must be contiguous")
+        if g.dtype not in _DTYPE_CODE:
+            raise RuntimeError(f"unsupported grad dtype {g.dtype}")
+
+
 class LayerAdam:
     """Layer-wise Adam/AdamW whose element update runs on the MI355X.
 
@@ -782,13 +816,7 @@ class LayerAdam:
         device = grads[0].device
         if device.type != 'cuda':
             raise RuntimeError("clip_grad_norm works on device tensors")
-        for g in grads:
-            if g.device != device:
-                raise RuntimeError("all grads must be on one device")
-            if not g.is_contiguous():
-                raise RuntimeError("grads must be contiguous")
-            if g.dtype not in _DTYPE_CODE:
-                raise RuntimeError(f"unsupported grad dtype {g.dtype}")
+        _check_grads(grads, device)
         nwork = _norm_workspace_elems(self.lib)
         with _on_device(device):
             s = _torch_stream(stream, device)
@@ -805,26 +833,8 @@ class LayerAdam:
             work, sqnorm, cn = base, base + nwork * 8, base + (nwork + 1) * 8
             pair = buf[nwork + 1:].view(torch.float32)
             coef, norm = pair[0:1], pair[1:2]
-            # runs of one dtype, at most LA_NORM_MULTI_MAX buffers each, one
-            # la_grad_norm_multi call per run (two launches): the first run
-            # overwrites the sum, later ones add to it, the last one also writes
-            # the coefficient
-            runs = []
-            for g in grads:
-                if runs and runs[-1][0].dtype == g.dtype and len(runs[-1]) < _lib.LA_NORM_MULTI_MAX:
-                    runs[-1].append(g)
-                else:
-                    runs.append([g])
-            for i, run in enumerate(runs):
-                flat = []
-                for g in run:
-                    flat += (g.data_ptr(), g.numel())
-                bufs = ctypes.cast((ctypes.c_uint64 * len(flat))(*flat), ctypes.POINTER(_lib.LaGradBuffer))
-                last = i == len(runs) - 1
-                rc = self.lib.la_grad_norm_multi(_DTYPE_CODE[run[0].dtype], bufs, len(run), work, nwork * 8, sqnorm,
-                                                 int(i > 0), float(max_norm), cn if last else None,
-                                                 cn + 4 if last else None, handle)
-                _lib.check(rc, "la_grad_norm_multi")
+            # the first run of buffers overwrites the sum, the last one writes the coefficient
+            _norm_runs(self.lib, grads, work, nwork, sqnorm, False, float(max_norm), cn, handle)
         return coef, norm
 
     def grad_norm_begin(self, device=None) -> "GradNormAccumulator":
@@ -842,7 +852,8 @@ class LayerAdam:
 
 class GradNormAccumulator:
     """Float64 sum of squares accumulated over several device buffers
-    (la_grad_sqnorm with accumulate), then one clip coefficient (la_clip_coef).
+    (la_grad_norm_multi with accumulate), then one clip coefficient
+    (la_clip_coef).
 
     One accumulator is one running sum: its ``add`` and ``finish`` calls must be
     ordered, i.e. on one stream or synchronised between streams.  Its scratch
@@ -859,19 +870,17 @@ class GradNormAccumulator:
         self.count = 0
 
     @torch.no_grad()
-    def add(self, grad: torch.Tensor, *, stream=None) -> None:
-        if grad.device != self.device:
-            raise RuntimeError(f"grad on {grad.device}, accumulator on {self.device}")
-        if not grad.is_contiguous():
-            raise RuntimeError("grads must be contiguous")
-        if grad.dtype not in _DTYPE_CODE:
-            raise RuntimeError(f"unsupported grad dtype {grad.dtype}")
-        with torch.cuda.device(self.device):
+    def add(self, grad, *, stream=None) -> None:
+        """Add one grad buffer, or a sequence of them (a layer's per-tensor
+        grads: two launches for up to 32 tensors of one dtype)."""
+        grads = [grad] if isinstance(grad, torch.Tensor) else [g for g in grad if g is not None]
+        if not grads:
+            return
+        _check_grads(grads, self.device)
+        with _on_device(self.device):
             s = _torch_stream(stream, self.device)
-            _lib.check(self.lib.la_grad_sqnorm(_DTYPE_CODE[grad.dtype], _ptr(grad), grad.numel(),
-                                               _ptr(self.work), self.work.numel() * 8, _ptr(self.sqnorm),
-                                               int(self.count > 0), s.cuda_stream),
-                       "la_grad_sqnorm")
+            _norm_runs(self.lib, grads, _ptr(self.work), self.work.numel(), _ptr(self.sqnorm), self.count > 0,
+                       0.0, None, s.cuda_stream)
             self.work.record_stream(s)
             self.sqnorm.record_stream(s)
         self.count += 1

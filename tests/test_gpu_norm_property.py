@@ -203,3 +203,33 @@ def test_clip_grad_norm_over_many_tensors_of_mixed_dtype(hip_device):
     c_ref, n_ref = O.clip_coef(float(norm.item()) ** 2, 0.05)
     assert abs(coef.item() - c_ref) <= 2 * float(np.spacing(np.float32(c_ref)))
     assert 0.0 < coef.item() < 1.0
+
+
+def test_accumulator_takes_lists_of_per_tensor_grads(hip_device):
+    """GradNormAccumulator.add with a layer's per-tensor grads (a list: runs of
+    one dtype through la_grad_norm_multi) and with single buffers, in sliding
+    order: the norm is the exact one rounded to fp32 (within one ulp)."""
+    from slideformer_amd import LayerAdam
+
+    rng = np.random.default_rng(41)
+    adam = LayerAdam()
+    acc = adam.grad_norm_begin(hip_device)
+    exact = 0.0
+    for layer in range(5):
+        kinds = ["bf16"] * 7 + ["f32"] * 3 if layer % 2 else ["bf16"] * 40
+        grads = []
+        for kind in kinds:
+            bits = _bits(rng.normal(0, 1e-3, int(rng.integers(0, 9000))), kind)
+            view = bits.view(np.float32) if kind == "f32" else bits
+            exact += O.grad_sqnorm(view, KIND16[kind])
+            grads.append(H.to_dev_bits(bits, kind, hip_device))
+        acc.add(grads if layer != 3 else grads[0])
+        if layer == 3:
+            for g in grads[1:]:
+                acc.add(g)
+    acc.add([])                                   # nothing to add
+    coef, norm = acc.finish(1e-3)
+    torch.cuda.synchronize()
+    want = np.float32(math.sqrt(exact))
+    assert abs(float(norm.item()) - float(want)) <= float(np.spacing(want))
+    assert 0.0 < coef.item() < 1.0
