@@ -670,8 +670,12 @@ class LayerAdam:
     # steps (layer_adam.py:270-468)
     # ------------------------------------------------------------------
     @torch.no_grad()
-    def step(self, layer_idx: int = None, closure=None):
-        """Update one layer (or all layers) from ``p.grad`` (layer_adam.py:271-359)."""
+    def step(self, layer_idx: int = None, closure=None, *, clip_coef=None):
+        """Update one layer (or all layers) from ``p.grad`` (layer_adam.py:271-359).
+
+        Keyword-only ``clip_coef``: a float32 device scalar (from
+        ``clip_grad_norm`` or a ``GradNormAccumulator``) that scales every grad
+        first, as in ``step_chunk``."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -692,15 +696,17 @@ class LayerAdam:
                 state = self.state[p]
                 assert p.numel() == g.numel(), "params and grads must have the same size"
                 entries.append((p, g, state['exp_avg'], state['exp_avg_sq']))
-            self._update_tensors(param_group, entries)
+            self._update_tensors(param_group, entries, clip_coef)
         self.synchronize()
         self._post_step(layer_idx)
         return loss
 
     @torch.no_grad()
     def step_with_grad_views(self, layer_idx: int = None,
-                             grad_views: Dict[torch.nn.Parameter, torch.Tensor] = None, closure=None):
-        """Like ``step`` but with grads from a ``{param: grad_view}`` dict (layer_adam.py:362-428)."""
+                             grad_views: Dict[torch.nn.Parameter, torch.Tensor] = None, closure=None, *,
+                             clip_coef=None):
+        """Like ``step`` but with grads from a ``{param: grad_view}`` dict
+        (layer_adam.py:362-428); ``clip_coef`` as in ``step``."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -722,7 +728,7 @@ class LayerAdam:
                 state = self.state[p]
                 assert p.numel() == grad.numel(), "params and grads must have the same size"
                 entries.append((p, grad, state['exp_avg'], state['exp_avg_sq']))
-            self._update_tensors(param_group, entries)
+            self._update_tensors(param_group, entries, clip_coef)
         self.synchronize()
         self._post_step(layer_idx)
         return loss
@@ -735,7 +741,7 @@ class LayerAdam:
                 with torch.cuda.device(streamer.device):
                     streamer.sync()
 
-    def _update_tensors(self, param_group, entries):
+    def _update_tensors(self, param_group, entries, clip_coef=None):
         """The per-tensor adam_update calls of step(layer) / step_with_grad_views
         (layer_adam.py:314-327, 397-410), in order.  Device tensors on one device
         with one registered dtype triple that pass every per-call check and do not
@@ -747,17 +753,22 @@ class LayerAdam:
         hp = (param_group['step'], param_group['lr'], beta1, beta2, param_group['eps'],
               param_group['weight_decay'], param_group['bias_correction'])
         segs = _segments(entries) if len(entries) > 1 else None
+        if segs is not None and clip_coef is not None:
+            p0 = entries[0][0]
+            if (clip_coef.dtype != torch.float32 or clip_coef.numel() < 1 or not clip_coef.is_cuda
+                    or clip_coef.get_device() != p0.get_device()):
+                segs = None                  # the per-call path raises the reference-style error
         if segs is not None:
             p0, g0, m0, _ = entries[0]
             with _on_device(p0.device):
                 rc = self.lib.la_adam_update_multi(
                     self.optimizer_id, int(hp[0]), hp[1], hp[2], hp[3], hp[4], hp[5], int(bool(hp[6])),
                     _DTYPE_CODE[p0.dtype], _DTYPE_CODE[g0.dtype], _DTYPE_CODE[m0.dtype], segs, len(entries),
-                    None, _stream_handle(None, p0.device))
+                    _ptr(clip_coef), _stream_handle(None, p0.device))
             _lib.check(rc, "la_adam_update_multi")
             return
         for p, g, m, v in entries:
-            self.adam_update(*hp, p, g, m, v)
+            self.adam_update(*hp, p, g, m, v, clip_coef=clip_coef)
 
     @torch.no_grad()
     def begin_chunk_step(self, layer_idx: int):

@@ -92,6 +92,51 @@ def test_step_per_tensor_and_grad_views(hip_device):
         assert np.array_equal(H.to_np_bits(st["exp_avg_sq"].reshape(-1), "f32"), v.view(np.uint32))
 
 
+@pytest.mark.parametrize("where", ["device", "host"])
+def test_step_per_tensor_with_clip_coef(where, hip_device):
+    """step(layer) and step_with_grad_views with the keyword-only clip_coef:
+    the layer's grads go through clip_grad_norm (one la_grad_norm_multi call)
+    and every tensor's update scales its grads by the coefficient, bit-exact
+    with the checker fed the same coefficient.  On host tensors the per-tensor
+    calls stream through HBM with the device coefficient."""
+    shapes = [(37, 5), (5,), (64, 3), (1,), (300, 7)]
+    rng = np.random.default_rng(12)
+    init = [rng.normal(0, 0.02, int(np.prod(s))).astype(np.float32) for s in shapes]
+    at = hip_device if where == "device" else "cpu"
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01)
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).view(s).to(at)) for x, s in zip(init, shapes)]
+    adam.add_layer_params(0, params)
+    orc = O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True)
+    hp = [x.copy() for x in init]
+    hm = [np.zeros_like(x) for x in init]
+    hv = [np.zeros_like(x) for x in init]
+    for step in range(1, 4):
+        grads = [torch.from_numpy(rng.normal(0, 1e-2, x.size).astype(np.float32)) for x in init]
+        if step % 2:
+            gbits = [g.numpy().copy() for g in grads]
+            for p, g, s in zip(params, grads, shapes):
+                p.grad = g.view(s).to(at)
+            coef, _ = adam.clip_grad_norm([g.to(hip_device) for g in grads], 1e-2)
+            adam.step(0, clip_coef=coef)
+        else:
+            grads = [g.bfloat16() for g in grads]
+            gbits = [H.to_np_bits(g, "bf16") for g in grads]
+            coef, _ = adam.clip_grad_norm([g.to(hip_device) for g in grads], 1e-2)
+            adam.step_with_grad_views(0, {p: g.view(s).to(at) for p, g, s in zip(params, grads, shapes)},
+                                      clip_coef=coef)
+        c = float(coef.item())
+        assert 0.0 < c < 1.0
+        for x, g, m, v in zip(hp, gbits, hm, hv):
+            orc.update(step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, x, g, m, v,
+                       g16="bf16" if g.dtype == np.uint16 else None, clip_coef=c)
+    torch.cuda.synchronize()
+    for p, x, m, v in zip(params, hp, hm, hv):
+        assert np.array_equal(H.to_np_bits(p.data.reshape(-1), "f32"), x.view(np.uint32))
+        st = adam.state[p]
+        assert np.array_equal(H.to_np_bits(st["exp_avg"].reshape(-1), "f32"), m.view(np.uint32))
+        assert np.array_equal(H.to_np_bits(st["exp_avg_sq"].reshape(-1), "f32"), v.view(np.uint32))
+
+
 def test_host_tensors_are_staged_through_hbm(hip_device):
     """The reference's layout (fp32 master + bf16 grads in host RAM) still works:
     the update runs on the GPU in 16 Mi-element pieces and the call returns after
