@@ -606,15 +606,16 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw16_kernel(StepArgs a)
 constexpr int kMaxSegs = 16;
 constexpr uint64_t kMaxSegScalars = 64;  // one wave's lanes
 // Segments of at least this many runs (256 elements each) get a launch of
-// la_adamw_kernel of their own: there every wave starts with its arguments
-// already in registers, while a wave of the multi kernel first searches its
-// segment and loads its arguments, latency that 16 resident waves per CU do
-// not hide.  Measured on MI355X: batching a Llama-3.1-8B layer's nine tensors
-// (16-58 Mi elements) costs 5 % against separate launches; with this cut
-// (4 Mi elements) they launch separately and a GPT-2 block's twelve tensors
-// (at most 2.4 Mi) still go in one launch.
+// la_adamw_kernel of their own.  No limit in the product build: with the
+// wave index and the segment arguments in scalar registers, a Llama-3.1-8B
+// layer's nine tensors (16-58 Mi elements) batched run 1.1-1.7 % faster than
+// separate launches of the big ones (step_with_grad_views 840-845 against
+// 851-853 us, step(layer) 911-912 against 925-929 us, MI355X), also against
+// batches that large at the single-call kernel's residency (936 / 848 us).
+// The small-grid test build sets it low, so that its tests still take the
+// separate launches.
 #ifndef LA_MULTI_OWN_LAUNCH_RUNS
-#define LA_MULTI_OWN_LAUNCH_RUNS 16384
+#define LA_MULTI_OWN_LAUNCH_RUNS (~0ull)
 #endif
 
 struct MultiArgs {
