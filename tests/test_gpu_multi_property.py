@@ -13,9 +13,10 @@ buffer (phases that agree or not), and it has a bf16 copy or none; each call
 has a clip coefficient or none.  Half the examples run on the small-grid
 test build of the library, where tensors of 2048 elements or more take their
 own launch and the update kernel's grid-stride loop runs (the product build
-does both only from 4 Mi elements and 2^34 elements on).  Every bit of every
-tensor's p, m, v and copy must equal the CPU checker replaying the same calls
-one tensor at a time, NaN as a class.  Examples are drawn from a fixed seed."""
+batches tensors of any size and strides only above 2^34 elements).  Every
+bit of every tensor's p, m, v and copy must equal the CPU checker replaying
+the same calls one tensor at a time, NaN as a class.  Examples are drawn
+from a fixed seed."""
 from __future__ import annotations
 
 import numpy as np

@@ -504,7 +504,7 @@ def test_single_call_beyond_2_pow_31_elements(hip_device):
 # several calls of one step in one launch (la_adam_update_multi)
 # ---------------------------------------------------------------------------
 
-# the last size is above the library's own-launch cut (16384 runs of 256 elements)
+# the last size: a 4 Mi-element segment batched with the small ones
 MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 2, 5000, 12, 129, 31, 8,
                16384 * 256 + 101]
 
@@ -512,9 +512,9 @@ MULTI_SIZES = [1, 3, 15, 16, 17, 255, 256, 257, 4099, 100_003, 7, 64, 1000, 33, 
 @pytest.mark.parametrize("mode", ["adamw", "l2", "none"])
 @pytest.mark.parametrize("triple", [("f32", "bf16", "f32"), ("f32", "f32", "f32"), ("bf16", "bf16", "bf16")])
 def test_multi_update_equals_separate_calls(triple, mode, hip_device):
-    """21 segments of awkward sizes: 19 small ones (two batched launches of up
-    to 16), one large one above the own-launch cut and one whose params are out
-    of phase with its grads (both launched on their own).  Some sit at odd
+    """21 segments of awkward sizes: 19 small ones and a 4 Mi-element one (two
+    batched launches of up to 16) and one whose params are out of phase with
+    its grads (launched on its own).  Some sit at odd
     element offsets inside their buffers; a clip coefficient applies and every
     other segment writes a bf16 copy.  Bit-exact with the same 21
     la_adam_update calls, and every segment with the oracle replaying them."""
@@ -575,7 +575,8 @@ def test_multi_update_equals_separate_calls(triple, mode, hip_device):
 # ---------------------------------------------------------------------------
 # launch paths the product build takes only at sizes beyond one GPU: the
 # small-grid test build (64 waves per update launch, 2 workgroups per norm
-# launch, own launches from 8 runs per segment) against the product build
+# launch, own launches from 8 runs per segment, which the product build never
+# gives a segment whose pointers agree in phase) against the product build
 # ---------------------------------------------------------------------------
 
 SMALL_GRID_SIZES = [7, 16, 64 * 256 * 3 + 5, 64 * 256 * 40 + 13, 1_000_003]
