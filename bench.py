@@ -958,6 +958,10 @@ def main():
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
                     help="c2 (default, the headline): one Llama-3.1-8B layer; c3 / c4: whole resident "
                          "model / 48-layer stack (prints its own JSON line)")
+    ap.add_argument("--shard", type=int, default=1,
+                    help="C2 only: time one GPU's share of a W-GPU data-parallel step, a contiguous 1/W "
+                         "slice of the layer (norm, clip, update; the all-reduce of the shards' sums and "
+                         "the collectives around the step are not run)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -996,8 +1000,12 @@ def main():
         return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    n = sum(LLAMA8B_LAYER)
-    log(f"device {torch.cuda.get_device_name(dev)}; C2 layer n={n}")
+    if args.shard < 1:
+        print("--shard needs W >= 1", file=sys.stderr)
+        sys.exit(2)
+    n = sum(LLAMA8B_LAYER) // args.shard
+    log(f"device {torch.cuda.get_device_name(dev)}; C2 layer n={n}" +
+        (f" (one shard of {args.shard})" if args.shard > 1 else ""))
 
     gen = torch.Generator(device=dev)
     gen.manual_seed(20)
@@ -1058,7 +1066,7 @@ def main():
     value = n / (ms_per_step * 1e-3) / 1e9
     achieved = BYTES_PER_PARAM_UPDATE * n / (upd_avg * 1e-3) / 1e9
     step_bytes = (BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0)) * n
-    traffic, traffic_source = read_traffic()
+    traffic, traffic_source = read_traffic() if args.shard == 1 else (None, None)
 
     result = {
         "metric": METRIC,
@@ -1079,6 +1087,7 @@ def main():
                          "wd 0.01) + bf16 compute copy" if clip else
                          "C2 layer, fused AdamW + bf16 copy only (no norm pass)"),
             "params": n,
+            "shard_of": args.shard,
             "grad_dtype": "bf16",
             "state_dtype": "f32",
             "bytes_per_param_step": BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0),
@@ -1100,7 +1109,10 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if args.cpu_budget > 0:
+    if args.shard > 1:
+        result["config"]["workload"] = (f"one GPU's 1/{args.shard} shard of the C2 layer ({n:,} params, "
+                                        "contiguous slice): " + result["config"]["workload"])
+    if args.cpu_budget > 0 and args.shard == 1:
         del p, m, v, g, out
         torch.cuda.empty_cache()
         log("timing the CPU baseline")
