@@ -71,7 +71,7 @@ def cases(draw):
                 steps=draw(st.lists(step(), min_size=1, max_size=3)), seed=draw(st.integers(0, 2**31 - 1)))
 
 
-@settings(max_examples=60, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@settings(max_examples=200, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
 @given(c=cases())
 def test_multi_update_equals_checker_on_random_layers(c, hip_device):
     print(f"multi property case: {c}", flush=True)

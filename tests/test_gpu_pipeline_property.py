@@ -49,7 +49,7 @@ def _place(t, host, pinned, dev):
     return t.pin_memory() if pinned else t.clone()
 
 
-@settings(max_examples=40, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@settings(max_examples=200, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
 @given(c=cases())
 def test_pipeline_equals_resident_on_random_layouts(c, hip_device):
     print(f"pipeline property case: {c}", flush=True)

@@ -69,7 +69,7 @@ def cases(draw):
                 calls=draw(st.lists(call(), min_size=1, max_size=4)), seed=draw(st.integers(0, 2**31 - 1)))
 
 
-@settings(max_examples=150, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@settings(max_examples=500, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
 @given(c=cases())
 def test_device_update_equals_checker_on_random_calls(c, hip_device):
     print(f"update property case: {c}", flush=True)
