@@ -19,6 +19,9 @@ import torch  # noqa: F401  (binds the HIP runtime before the library is loaded)
 # where slideformer_amd/build.py writes the library
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libslideformer_amd.so")
 
+# LA_ABI_VERSION of include/layer_adam.h that these bindings declare
+ABI_VERSION = 9
+
 LA_OK = 0
 LA_EINVAL = -22
 LA_EDTYPE = -95
@@ -205,7 +208,14 @@ def load(path: str | None = None):
             raise ImportError(
                 f"slideformer_amd HIP library not found at {path}; build it with "
                 "`python -m slideformer_amd.build` (there is no CPU fallback)")
-        _lib = _declare(ctypes.CDLL(path))
+        raw = ctypes.CDLL(path)
+        raw.la_abi_version.restype = ctypes.c_int
+        found = raw.la_abi_version()
+        if found != ABI_VERSION:
+            raise ImportError(
+                f"{path} implements the C-ABI version {found}, this package needs {ABI_VERSION}; rebuild it "
+                "with `python -m slideformer_amd.build`")
+        _lib = _declare(raw)
         return _lib
 
 

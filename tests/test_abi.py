@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     version = int(re.search(r"#define LA_ABI_VERSION (\d+)", _read(HEADER)).group(1))
-    assert L.la_abi_version() == version == 9
+    assert L.la_abi_version() == version == _lib.ABI_VERSION == 9
     header = _read(HEADER)
     for name in ("LA_OK", "LA_EINVAL", "LA_EDTYPE", "LA_ENOMEM", "LA_ERANGE", "LA_EFAULT", "LA_F32", "LA_BF16", "LA_F16", "LA_ON_HOST_P",
                  "LA_ON_HOST_M", "LA_ON_HOST_V", "LA_ON_HOST_G", "LA_ON_HOST_OUT", "LA_ON_HOST_ALL",
@@ -332,3 +332,26 @@ def test_header_is_usable_from_c(tmp_path):
         got = np.array([float.fromhex(x) for x in f[1:7]], dtype=np.float32)
         assert np.array_equal(got.view(np.uint32), r[:6].view(np.uint32)), (st, got, r[:6])
         assert int(f[7]) == 2
+
+
+def test_library_of_another_abi_version_is_refused(tmp_path):
+    """A library built from other sources (here a stand-in that only reports ABI
+    version 1) is refused at load with a message to rebuild, before any of its
+    symbols is bound."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "old.c"
+    src.write_text("int la_abi_version(void) { return 1; }\n")
+    so = tmp_path / "libold.so"
+    subprocess.run([gcc, "-shared", "-fPIC", "-o", str(so), str(src)], check=True)
+    saved = _lib._lib
+    _lib._lib = None
+    try:
+        with pytest.raises(ImportError, match="C-ABI version 1"):
+            _lib.load(str(so))
+    finally:
+        _lib._lib = saved
