@@ -10,7 +10,10 @@ in HBM before the timed region starts.
 Prints ONE JSON line (rank 0).  ``value`` = params / step time (Gparams/s).
 ``roofline`` covers the dominant kernel (the update): algorithmic bytes = 28 B
 per param (read p4 g2 m4 v4, write p4 m4 v4 + bf16 copy 2) / its average
-duration measured with HIP events on its stream inside the timed region.
+duration measured with HIP events on its stream inside the timed region;
+``roofline.traffic`` is that kernel's HBM bytes per launch, measured in the
+same run with two rocprofv3 --pmc passes over a short child run (the L2's
+sized read and write requests), before this process touches the GPU.
 ``cpu_baseline`` times the reference CPU Adam (compiled from its own sources
 into oracle/_ref, or the C restatement in oracle/ when that is absent) on this
 host, on the same layer size.
@@ -58,6 +61,74 @@ def read_traffic():
     source = (f"{os.path.relpath(TRAFFIC_SUMMARY, REPO)}: rocprofv3 --pmc sized L2 read/write request "
               f"counters (TCC_EA0_RDREQ_128B/64B/32B, TCC_EA0_WRREQ/WRREQ_64B), kernel build {build}")
     return value, source
+
+
+UPDATE_KERNEL_RE = r"la_adamw_kernel<float, [^<>]*bf16_t, float>"
+READ_COUNTERS = ("TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_32B_sum")
+WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def traffic_live(timeout_s: float = 150.0):
+    """(HBM bytes per update launch, where they come from), measured now, or
+    (None, reason).  Two rocprofv3 --pmc passes, each over a short run of this
+    script as a child process (started before this process touches the GPU):
+    the L2's read requests by size, then its write requests.  Bytes = 128 x
+    RDREQ_128B + 64 x RDREQ_64B + 32 x RDREQ_32B + 64 x WRREQ_64B + 32 x
+    (WRREQ - WRREQ_64B), averaged over the update kernel's dispatches."""
+    import csv
+    import glob
+    import re
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
+                                         else None)
+    if prof is None:
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="la_traffic_", dir="/tmp" if os.path.isdir("/tmp") else None)
+    env = dict(os.environ, TMPDIR=os.path.dirname(tmp))
+    vals, ndisp = {}, 0
+    try:
+        for k, counters in enumerate((READ_COUNTERS, WRITE_COUNTERS)):
+            out = os.path.join(tmp, f"p{k}")
+            cmd = [prof, "--pmc", *counters, "-d", out, "-o", f"p{k}", "--output-format", "csv", "--",
+                   sys.executable, os.path.abspath(__file__), "--steps", "2", "--warmup", "1", "--cpu-budget", "0",
+                   "--traffic", "profile"]
+            log(f"traffic pass {k + 1}/2: rocprofv3 --pmc {' '.join(counters)}")
+            child = subprocess.Popen(cmd, cwd=tmp, env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                                     start_new_session=True)
+            try:
+                child.wait(timeout=timeout_s)
+            except subprocess.TimeoutExpired:
+                os.killpg(child.pid, signal.SIGKILL)
+                child.wait()
+                return None, f"rocprofv3 pass {k + 1} timed out"
+            # the profiler can end with a signal after the program finished: the files decide
+            files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                return None, f"rocprofv3 pass {k + 1} wrote no counters (exit status {child.returncode})"
+            per = {c: [] for c in counters}
+            with open(files[0]) as fh:
+                for row in csv.DictReader(fh):
+                    if re.search(UPDATE_KERNEL_RE, row["Kernel_Name"]) and row["Counter_Name"] in per:
+                        per[row["Counter_Name"]].append(float(row["Counter_Value"]))
+            for c in counters:
+                if not per[c]:
+                    return None, f"rocprofv3 pass {k + 1}: no {c} for the update kernel"
+                vals[c] = sum(per[c]) / len(per[c])
+            ndisp = len(per[counters[0]])
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    read = (128 * vals["TCC_EA0_RDREQ_128B_sum"] + 64 * vals["TCC_EA0_RDREQ_64B_sum"]
+            + 32 * vals["TCC_EA0_RDREQ_32B_sum"])
+    w64 = vals["TCC_EA0_WRREQ_64B_sum"]
+    write = 64 * w64 + 32 * (vals["TCC_EA0_WRREQ_sum"] - w64)
+    source = (f"measured in this run: rocprofv3 --pmc over a 2-step run of this build, {ndisp} update dispatches "
+              f"per pass; read {read:.0f} B (128/64/32 B x TCC_EA0_RDREQ_128B/64B/32B), write {write:.0f} B "
+              "(64 B x TCC_EA0_WRREQ_64B + 32 B x the rest)")
+    return read + write, source
 
 
 def cpu_baseline(n: int, budget_s: float):
@@ -958,6 +1029,10 @@ def main():
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
                     help="c2 (default, the headline): one Llama-3.1-8B layer; c3 / c4: whole resident "
                          "model / 48-layer stack (prints its own JSON line)")
+    ap.add_argument("--traffic", choices=["live", "profile"], default="live",
+                    help="roofline.traffic of the C2 line: measured now with two rocprofv3 --pmc passes "
+                         "(live, ~20 s; falls back to the committed profile if that fails), or read from "
+                         "profiles/la_adamw_kernel_c2_traffic.txt (profile)")
     ap.add_argument("--shard", type=int, default=1,
                     help="C2 only: time one GPU's share of a W-GPU data-parallel step, a contiguous 1/W "
                          "slice of the layer (norm, clip, update; the all-reduce of the shards' sums and "
@@ -975,6 +1050,14 @@ def main():
     if args.disk_bench:
         disk_bench(args)
         return
+
+    # the traffic passes run as child processes before this process touches the GPU
+    live = None
+    if (args.traffic == "live" and not (args.streamed or args.step_api or args.copy_ceiling or args.triples)
+            and args.config == "c2" and args.shard == 1 and not args.no_clip):
+        live = traffic_live()
+        if live[0] is None:
+            log(f"live traffic unavailable ({live[1]}); using the committed profile")
 
     import torch
 
@@ -1066,7 +1149,12 @@ def main():
     value = n / (ms_per_step * 1e-3) / 1e9
     achieved = BYTES_PER_PARAM_UPDATE * n / (upd_avg * 1e-3) / 1e9
     step_bytes = (BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0)) * n
-    traffic, traffic_source = read_traffic() if args.shard == 1 else (None, None)
+    if live is not None and live[0] is not None:
+        traffic, traffic_source = live
+    elif args.shard == 1:
+        traffic, traffic_source = read_traffic()
+    else:
+        traffic, traffic_source = None, None
 
     result = {
         "metric": METRIC,
