@@ -68,6 +68,31 @@ READ_COUNTERS = ("TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDR
 WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
 
 
+def update_kernel_counters(path: str, counters):
+    """({counter: mean per dispatch}, dispatches) of the update kernel in one
+    rocprofv3 counter_collection.csv, or a message naming what is missing."""
+    import csv
+    import re
+
+    per = {c: [] for c in counters}
+    with open(path) as fh:
+        for row in csv.DictReader(fh):
+            if re.search(UPDATE_KERNEL_RE, row["Kernel_Name"]) and row["Counter_Name"] in per:
+                per[row["Counter_Name"]].append(float(row["Counter_Value"]))
+    for c in counters:
+        if not per[c]:
+            return f"no {c} for the update kernel"
+    return {c: sum(v) / len(v) for c, v in per.items()}, len(per[counters[0]])
+
+
+def traffic_bytes(vals):
+    """(read, write) HBM bytes from the L2's sized request counts."""
+    read = (128 * vals["TCC_EA0_RDREQ_128B_sum"] + 64 * vals["TCC_EA0_RDREQ_64B_sum"]
+            + 32 * vals["TCC_EA0_RDREQ_32B_sum"])
+    w64 = vals["TCC_EA0_WRREQ_64B_sum"]
+    return read, 64 * w64 + 32 * (vals["TCC_EA0_WRREQ_sum"] - w64)
+
+
 def traffic_live(timeout_s: float = 150.0):
     """(HBM bytes per update launch, where they come from), measured now, or
     (None, reason).  Two rocprofv3 --pmc passes, each over a short run of this
@@ -75,9 +100,7 @@ def traffic_live(timeout_s: float = 150.0):
     the L2's read requests by size, then its write requests.  Bytes = 128 x
     RDREQ_128B + 64 x RDREQ_64B + 32 x RDREQ_32B + 64 x WRREQ_64B + 32 x
     (WRREQ - WRREQ_64B), averaged over the update kernel's dispatches."""
-    import csv
     import glob
-    import re
     import shutil
     import signal
     import subprocess
@@ -109,22 +132,14 @@ def traffic_live(timeout_s: float = 150.0):
             files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
             if not files:
                 return None, f"rocprofv3 pass {k + 1} wrote no counters (exit status {child.returncode})"
-            per = {c: [] for c in counters}
-            with open(files[0]) as fh:
-                for row in csv.DictReader(fh):
-                    if re.search(UPDATE_KERNEL_RE, row["Kernel_Name"]) and row["Counter_Name"] in per:
-                        per[row["Counter_Name"]].append(float(row["Counter_Value"]))
-            for c in counters:
-                if not per[c]:
-                    return None, f"rocprofv3 pass {k + 1}: no {c} for the update kernel"
-                vals[c] = sum(per[c]) / len(per[c])
-            ndisp = len(per[counters[0]])
+            got = update_kernel_counters(files[0], counters)
+            if isinstance(got, str):
+                return None, f"rocprofv3 pass {k + 1}: {got}"
+            vals.update(got[0])
+            ndisp = got[1]
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
-    read = (128 * vals["TCC_EA0_RDREQ_128B_sum"] + 64 * vals["TCC_EA0_RDREQ_64B_sum"]
-            + 32 * vals["TCC_EA0_RDREQ_32B_sum"])
-    w64 = vals["TCC_EA0_WRREQ_64B_sum"]
-    write = 64 * w64 + 32 * (vals["TCC_EA0_WRREQ_sum"] - w64)
+    read, write = traffic_bytes(vals)
     source = (f"measured in this run: rocprofv3 --pmc over a 2-step run of this build, {ndisp} update dispatches "
               f"per pass; read {read:.0f} B (128/64/32 B x TCC_EA0_RDREQ_128B/64B/32B), write {write:.0f} B "
               "(64 B x TCC_EA0_WRREQ_64B + 32 B x the rest)")
