@@ -1068,9 +1068,15 @@ def main():
 
     # the traffic passes run as child processes before this process touches the GPU
     live = None
+    under_profiler = ("rocprof" in os.environ.get("LD_PRELOAD", "") or "ROCP_TOOL_LIBRARIES" in os.environ
+                      or "ROCPROF_OUTPUT_PATH" in os.environ)
     if (args.traffic == "live" and not (args.streamed or args.step_api or args.copy_ceiling or args.triples)
             and args.config == "c2" and args.shard == 1 and not args.no_clip):
-        live = traffic_live()
+        if under_profiler:
+            # no profiler runs of our own under another one: the committed profile serves
+            log("running under a profiler: roofline.traffic from the committed profile")
+        else:
+            live = traffic_live()
         if live[0] is None:
             log(f"live traffic unavailable ({live[1]}); using the committed profile")
 
