@@ -294,14 +294,25 @@ def _norm_runs(lib, grads, work, nwork, sqnorm, accumulate, max_norm, cn, handle
         else:
             runs.append([g])
     for i, run in enumerate(runs):
+        last = cn is not None and i == len(runs) - 1
+        acc = int(accumulate or i > 0)
+        code = _DTYPE_CODE[run[0].dtype]
+        if len(run) == 1:
+            # one buffer: the single-buffer entry points (the same bits, a smaller launch)
+            g = run[0]
+            if last:
+                rc = lib.la_grad_norm_clip(code, g.data_ptr(), g.numel(), work, nwork * 8, sqnorm, acc, max_norm, cn,
+                                           cn + 4, handle)
+            else:
+                rc = lib.la_grad_sqnorm(code, g.data_ptr(), g.numel(), work, nwork * 8, sqnorm, acc, handle)
+            _lib.check(rc, "la_grad_sqnorm")
+            continue
         flat = []
         for g in run:
             flat += (g.data_ptr(), g.numel())
         bufs = ctypes.cast((ctypes.c_uint64 * len(flat))(*flat), ctypes.POINTER(_lib.LaGradBuffer))
-        last = cn is not None and i == len(runs) - 1
-        rc = lib.la_grad_norm_multi(_DTYPE_CODE[run[0].dtype], bufs, len(run), work, nwork * 8, sqnorm,
-                                    int(accumulate or i > 0), max_norm, cn if last else None,
-                                    cn + 4 if last else None, handle)
+        rc = lib.la_grad_norm_multi(code, bufs, len(run), work, nwork * 8, sqnorm, acc, max_norm,
+                                    cn if last else None, cn + 4 if last else None, handle)
         _lib.check(rc, "la_grad_norm_multi")
 
 
