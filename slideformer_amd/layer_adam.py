@@ -284,9 +284,10 @@ def _norm_workspace_elems(lib) -> int:
 def _norm_runs(lib, grads, work, nwork, sqnorm, accumulate, max_norm, cn, handle):
     """The sum of squares of ``grads`` into the float64 at ``sqnorm`` (added to
     it when ``accumulate``): runs of one dtype, at most LA_NORM_MULTI_MAX
-    buffers each, one la_grad_norm_multi call (two launches) per run, later
-    runs adding to the earlier ones.  With ``cn`` (address of two fp32: coef,
-    norm) the last call also writes the clip coefficient."""
+    buffers each, one library call (two launches) per run, later runs adding
+    to the earlier ones: la_grad_norm_multi for a run of several buffers,
+    la_grad_sqnorm / la_grad_norm_clip for a run of one.  With ``cn`` (address
+    of two fp32: coef, norm) the last call also writes the clip coefficient."""
     runs = []
     for g in grads:
         if runs and runs[-1][0].dtype == g.dtype and len(runs[-1]) < _lib.LA_NORM_MULTI_MAX:
@@ -874,8 +875,8 @@ class LayerAdam:
 
 class GradNormAccumulator:
     """Float64 sum of squares accumulated over several device buffers
-    (la_grad_norm_multi with accumulate), then one clip coefficient
-    (la_clip_coef).
+    (la_grad_sqnorm, or la_grad_norm_multi for a list of them, with
+    accumulate), then one clip coefficient (la_clip_coef).
 
     One accumulator is one running sum: its ``add`` and ``finish`` calls must be
     ordered, i.e. on one stream or synchronised between streams.  Its scratch
