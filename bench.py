@@ -93,6 +93,12 @@ def traffic_bytes(vals):
     return read, 64 * w64 + 32 * (vals["TCC_EA0_WRREQ_sum"] - w64)
 
 
+def under_profiler() -> bool:
+    """Whether this process runs under rocprofv3 (its tool library is preloaded)."""
+    return ("rocprof" in os.environ.get("LD_PRELOAD", "") or "ROCP_TOOL_LIBRARIES" in os.environ
+            or "ROCPROF_OUTPUT_PATH" in os.environ)
+
+
 def traffic_live(timeout_s: float = 150.0):
     """(HBM bytes per update launch, where they come from), measured now, or
     (None, reason).  Two rocprofv3 --pmc passes, each over a short run of this
@@ -146,9 +152,10 @@ def traffic_live(timeout_s: float = 150.0):
     return read + write, source
 
 
-def cpu_baseline(n: int, budget_s: float):
+def cpu_baseline(n: int, budget_s: float, stands_for: str = ""):
     """Reference CPU Adam on this host: 28 B/param model, whole-layer steps
-    (methodology of bench/cpu_adam_profile/cpu_adam_benchmark.py:392-428)."""
+    (methodology of bench/cpu_adam_profile/cpu_adam_benchmark.py:392-428).
+    ``stands_for`` names the larger workload that n elements sample, if any."""
     import numpy as np
     import torch
 
@@ -156,6 +163,7 @@ def cpu_baseline(n: int, budget_s: float):
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
+    log(f"CPU baseline: {n} params, {threads} threads, about {budget_s:.0f} s of timing")
     cpu_model = "unknown"
     try:
         with open("/proc/cpuinfo") as fh:
@@ -168,10 +176,11 @@ def cpu_baseline(n: int, budget_s: float):
     usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     ref = O.load_ref()
     kind = "reference" if ref is not None else "port"
-    p = torch.randn(n) * 0.02
+    # in-place scaling: a fresh result tensor per operation would add its first-touch cost
+    p = torch.randn(n).mul_(0.02)
     m = torch.zeros(n)
     v = torch.zeros(n)
-    g = (torch.randn(n) * 1e-3).bfloat16()
+    g = torch.randn(n).mul_(1e-3).bfloat16()
     staging = torch.empty(n, dtype=torch.bfloat16)
     if ref is not None:
         ref.create_adam(0, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
@@ -209,7 +218,7 @@ def cpu_baseline(n: int, budget_s: float):
         "kind": kind,
         "sample": (f"{len(times)} whole-layer steps of {n} params (AdamW, fp32 p/m/v, bf16 grads) "
                    f"+ torch fp32->bf16 copy_, {threads} OpenMP threads on "
-                   f"{os.cpu_count()} visible CPUs"),
+                   f"{os.cpu_count()} visible CPUs" + (f"; {stands_for}" if stands_for else "")),
         "cpu_model": cpu_model,
         "nproc": os.cpu_count(),
         "usable_cpus": usable,
@@ -446,8 +455,23 @@ def streamed(args):
         },
         "stream_spans_ms": ({"h2d": round(st.h2d_ms, 3), "update": round(st.compute_ms, 3),
                              "d2h": round(st.d2h_ms, 3)} if st is not None and call == n else None),
+        "cpu_baseline": None,
     }
+    if args.cpu_budget > 0:
+        # the reference's CPU Adam on the same layer size, on this host, in this run
+        del p, m, v, g, out, state, host
+        adam = None
+        torch.cuda.empty_cache()
+        add_cpu_baseline(res, n, args.cpu_budget)
     print(json.dumps(res), flush=True)
+
+
+def add_cpu_baseline(res, n, budget_s, stands_for=""):
+    """Time the reference CPU Adam on n params into res["cpu_baseline"], and
+    the GPU line's rate over it into res["vs_cpu_baseline"]."""
+    log("timing the CPU baseline")
+    res["cpu_baseline"] = cpu_baseline(n, budget_s, stands_for)
+    res["vs_cpu_baseline"] = round(res["value"] / res["cpu_baseline"]["value"], 3)
 
 
 def copy_ceiling(args):
@@ -704,7 +728,15 @@ def streamed_model(args):
         "host_copy_ms_per_step": round(span_sum[3] / len(walls), 1),
         "host_threads": adam._streamers[dev].host_threads or "default (up to 16)",
         "wall_clock": "host perf_counter around the whole step (norm, clip, every layer's streamed update)",
+        "cpu_baseline": None,
     }
+    if args.cpu_budget > 0:
+        # the CPU Adam's rate per param does not depend on the buffer size beyond
+        # the caches: one decoder layer samples the whole model
+        layer = sum(LLAMA8B_LAYER)
+        add_cpu_baseline(res, layer, args.cpu_budget,
+                         f"sample of the whole C3 model: one of its decoder layers ({layer} of {n_total} params)")
+        res["cpu_baseline"]["whole_model_s_at_this_rate"] = round(n_total / (res["cpu_baseline"]["value"] * 1e9), 3)
     print(json.dumps(res), flush=True)
 
 
@@ -1067,14 +1099,12 @@ def main():
         return
 
     # the traffic passes run as child processes before this process touches the GPU
-    live = None
-    under_profiler = ("rocprof" in os.environ.get("LD_PRELOAD", "") or "ROCP_TOOL_LIBRARIES" in os.environ
-                      or "ROCPROF_OUTPUT_PATH" in os.environ)
+    live = (None, "not measured for this workload")
     if (args.traffic == "live" and not (args.streamed or args.step_api or args.copy_ceiling or args.triples)
             and args.config == "c2" and args.shard == 1 and not args.no_clip):
-        if under_profiler:
+        if under_profiler():
             # no profiler runs of our own under another one: the committed profile serves
-            log("running under a profiler: roofline.traffic from the committed profile")
+            live = (None, "running under a profiler")
         else:
             live = traffic_live()
         if live[0] is None:
@@ -1167,10 +1197,33 @@ def main():
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, update kernel avg {upd_avg:.4f} ms "
         f"(min {upd_ms[0]:.4f}, max {upd_ms[-1]:.4f})")
 
+    # The same update launch with none of its grads in the 256 MB memory-side
+    # cache (MALL): the grad-norm pass before each timed update above leaves up
+    # to 256 MB of the grads there.  Here a plain in-place pass over 1 GiB of
+    # other memory runs before each update instead, so the MALL holds that
+    # memory when the update starts.  Outside the timed steps above.
+    upd_nomall = None
+    if clip and args.steps > 0:
+        coef_last, _ = adam.clip_grad_norm([g], 1.0, stream=stream)
+        flush = torch.zeros(256 * 1024 * 1024, device=dev)
+        evs2 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.steps)]
+        for i in range(args.steps):
+            t += 1
+            flush.add_(1.0)
+            evs2[i][0].record(stream)
+            adam.step_chunk(p, g, m, v, dict(adam.defaults, step=t), bf16_out=out, clip_coef=coef_last,
+                            stream=stream)
+            evs2[i][1].record(stream)
+        torch.cuda.synchronize()
+        upd_nomall = sum(a.elapsed_time(b) for a, b in evs2) / args.steps
+        del flush
+        log(f"update kernel with the MALL flushed before each launch: avg {upd_nomall:.4f} ms")
+
     value = n / (ms_per_step * 1e-3) / 1e9
     achieved = BYTES_PER_PARAM_UPDATE * n / (upd_avg * 1e-3) / 1e9
     step_bytes = (BYTES_PER_PARAM_UPDATE + (BYTES_PER_PARAM_NORM if clip else 0)) * n
-    if live is not None and live[0] is not None:
+    if live[0] is not None:
         traffic, traffic_source = live
     elif args.shard == 1:
         traffic, traffic_source = read_traffic()
@@ -1205,6 +1258,8 @@ def main():
         "hbm_frac_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         "update_kernel_ms": round(upd_avg, 4),
         "update_gparams_s": round(n / (upd_avg * 1e-3) / 1e9, 3),
+        # the update with no grads in the MALL (a 1 GiB pass over other memory before each launch)
+        "update_kernel_ms_no_mall": round(upd_nomall, 4) if upd_nomall is not None else None,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -1215,6 +1270,16 @@ def main():
             "traffic_source": traffic_source,
             "kernel": "la_adamw_kernel<float, bf16_t, float>",
             "algorithmic_bytes_per_launch": BYTES_PER_PARAM_UPDATE * n,
+            # the clipped step's grad-norm pass leaves up to 256 MB of the grads in the MALL,
+            # and `achieved` counts those bytes; these two time the launch with the MALL
+            # holding other memory
+            "achieved_no_mall": (round(BYTES_PER_PARAM_UPDATE * n / (upd_nomall * 1e-3) / 1e9, 1)
+                                 if upd_nomall is not None else None),
+            "frac_no_mall": (round(BYTES_PER_PARAM_UPDATE * n / (upd_nomall * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+                             if upd_nomall is not None else None),
+            "mall_note": ("traffic counts L2-to-fabric requests, every one addressed to HBM; the MALL "
+                          "(256 MB memory-side cache) serves some of the grad reads in the timed steps, "
+                          "and these counters cannot tell those apart"),
         },
         "cpu_baseline": None,
     }

@@ -117,9 +117,10 @@ int la_adam_update(int id, uint64_t step, float lr, float beta1, float beta2, fl
  * and element types, as LayerAdam.step(layer) and step_with_grad_views make
  * them (layer_adam.py:299-327, 391-422).  Exactly equivalent to count
  * la_adam_update calls: the beta-power state advances once per segment (also
- * for n = 0), and each segment keeps its own scalar tail.  All segments are
- * launched together (one launch per 16 segments), so the segments must not
- * overlap in memory.  Every pointer is checked before anything changes; an
+ * for n = 0), and each segment keeps its own scalar tail.  Segments are
+ * launched together (one launch per 16 segments; a segment of more than
+ * 2^33 elements gets a grid-stride launch of its own), so the segments must
+ * not overlap in memory.  Every pointer is checked before anything changes; an
  * unregistered dtype triple advances the state once and returns LA_EDTYPE,
  * as the first of the separate calls would.
  */
@@ -196,7 +197,9 @@ int la_grad_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, voi
  * allocates nothing (no hipMalloc, no hipFree, no allocating library call).
  * Stage 1 of this build never uses more than 256 workgroups, so every n fits;
  * a build whose stage-1 grid could outgrow the array returns LA_ERANGE for
- * such n.  Runs on the current device; `stream` must belong to it.  Every
+ * such n.  Runs on the current device; `stream` must belong to it (NULL and
+ * the per-thread default stream do): a stream of another device is refused
+ * with LA_EINVAL before any launch.  Every
  * call on one GPU shares that GPU's array, which keeps the last call's
  * partials: calls that overlap on one GPU (streams not ordered with each
  * other) race.  The results are bit-identical to la_grad_norm_clip's for the

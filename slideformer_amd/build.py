@@ -68,11 +68,13 @@ def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: boo
 
 # A build with tiny grid caps, loaded only by the GPU tests: the update kernel's
 # grid-stride loop (taken by the product build only above 2^34 elements per
-# call), the own-launch path of la_adam_update_multi for small segments and
-# the grad norm's many-trip loop then run at test sizes.  Same sources, same
-# flags; only these launch limits differ.
+# call), la_adam_update_multi's batch splits and the own grid-stride launch of
+# a segment too large for one batch (above LA_MAX_GRID / 2 runs: 2^33 elements
+# in the product build, 32 runs = 8192 elements here) and the grad norm's
+# many-trip loop then run at test sizes.  Same sources, same flags; only these
+# launch limits differ.
 SMALL_GRID_LIB = os.path.join(LIB_DIR, "libslideformer_amd_smallgrid.so")
-SMALL_GRID_DEFINES = {"LA_MAX_GRID": 64, "LA_NORM_MAX_GRID": 2, "LA_MULTI_OWN_LAUNCH_RUNS": 8}
+SMALL_GRID_DEFINES = {"LA_MAX_GRID": 64, "LA_NORM_MAX_GRID": 2}
 
 
 # A plain C program that runs the step on the GPU through the C-ABI alone

@@ -605,18 +605,16 @@ __global__ __launch_bounds__(LA_BLOCK) void la_adamw16_kernel(StepArgs a)
 // overlap in memory.
 constexpr int kMaxSegs = 16;
 constexpr uint64_t kMaxSegScalars = 64;  // one wave's lanes
-// Segments of at least this many runs (256 elements each) get a launch of
-// la_adamw_kernel of their own.  No limit in the product build: with the
-// wave index and the segment arguments in scalar registers, a Llama-3.1-8B
-// layer's nine tensors (16-58 Mi elements) batched run 1.1-1.7 % faster than
-// separate launches of the big ones (step_with_grad_views 840-845 against
-// 851-853 us, step(layer) 911-912 against 925-929 us, MI355X), also against
-// batches that large at the single-call kernel's residency (936 / 848 us).
-// The small-grid test build sets it low, so that its tests still take the
-// separate launches.
-#ifndef LA_MULTI_OWN_LAUNCH_RUNS
-#define LA_MULTI_OWN_LAUNCH_RUNS (~0ull)
-#endif
+// Segments of any size go in a batch: with the wave index and the segment
+// arguments in scalar registers, a Llama-3.1-8B layer's nine tensors (16-58 Mi
+// elements) batched run 1.1-1.7 % faster than separate launches of the big
+// ones (step_with_grad_views 840-845 against 851-853 us, step(layer) 911-912
+// against 925-929 us, MI355X), also against batches that large at the
+// single-call kernel's residency (936 / 848 us).  The kernel has no
+// grid-stride loop, one wave per run, so a batch holds at most LA_MAX_GRID / 2
+// runs; a segment of more runs than that takes la_adamw_kernel's grid-stride
+// launch of its own (above 2^33 elements in the product build; the small-grid
+// test build, LA_MAX_GRID 64, takes it from 32 runs).
 
 struct MultiArgs {
     const float* coef;
@@ -938,7 +936,21 @@ template <typename TP, typename TG, typename TS> constexpr uint32_t multi_lds_by
 #endif
 }
 
+// Launch of la_adamw_kernel for the 4-element layout of `a`.
+template <typename TP, typename TG, typename TS> int launch4(const StepArgs& a, hipStream_t stream)
+{
+    const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
+    // lanes needed: every wave takes one run of 64 groups
+    const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
+    const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
+    return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
+                  update_lds_bytes<TP, TG, TS>(), stream, a);
+}
+
 // The all-16-bit path: the call's groups are re-laid out as 8-element groups.
+// Pointers that share a 4-element phase but not an 8-element one (16-byte
+// alignment) keep the 4-element layout of la_adamw_kernel rather than the
+// all-scalar path.
 template <typename T> int launch16(const StepArgs& a4, hipStream_t stream)
 {
     StepArgs a = a4;
@@ -948,6 +960,7 @@ template <typename T> int launch16(const StepArgs& a4, hipStream_t stream)
     const int bytes[5] = {2, 2, 2, 2, 2};
     const int h = common_head(addr, bytes, a.out ? 5 : 4, kVec16);
     if (h < 0 || static_cast<uint64_t>(h) >= a.tail_start) {
+        if (a4.nvec > 0) return launch4<T, T, T>(a4, stream);
         a.head = 0;
         a.nvec = 0;
     } else {
@@ -967,12 +980,7 @@ template <typename TP, typename TG, typename TS> struct StepLauncher {
         if constexpr (LA_WIDE16 && std::is_same<TP, TG>::value && std::is_same<TP, TS>::value &&
                       !std::is_same<TP, float>::value)
             return launch16<TP>(a, stream);
-        const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-        // lanes needed: every wave takes one run of 64 groups
-        const uint64_t vec_lanes = (a.nvec + 63) / 64 * 64;
-        const uint64_t work = vec_lanes > nscalar ? vec_lanes : nscalar;
-        return launch(la_adamw_kernel<TP, TG, TS>, dim3(grid_for(work, LA_BLOCK, LA_MAX_GRID)), dim3(LA_BLOCK),
-                      update_lds_bytes<TP, TG, TS>(), stream, a);
+        return launch4<TP, TG, TS>(a, stream);
     }
 };
 
@@ -1254,18 +1262,15 @@ constexpr uint64_t kScratchBytes = static_cast<uint64_t>(LA_NORM_SCRATCH_PARTIAL
 std::mutex g_scratch_mu;
 std::unordered_map<int, double*> g_scratch_ptr;  // device ordinal -> that device's copy of `scratch`
 
-// The address of `scratch` on the current device, looked up once per device
-// with that device current.
-int scratch_on_current_device(double** out)
+// The address of `scratch` on device `dev`, which is the current device,
+// looked up once per device with that device current.
+int scratch_on_current_device(int dev, double** out)
 {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_rc(e);
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     auto it = g_scratch_ptr.find(dev);
     if (it == g_scratch_ptr.end()) {
         void* ptr = nullptr;
-        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_rc(e);
         if (!ptr) return LA_EINVAL;
         it = g_scratch_ptr.emplace(dev, static_cast<double*>(ptr)).first;
@@ -1414,6 +1419,8 @@ try {
     uint64_t runs = 0;
     auto flush = [&]() -> int {
         if (batch.count == 0) return LA_OK;
+        // one wave per run and per segment: the grid must fit the dispatch packet
+        if (runs + batch.count > static_cast<uint64_t>(LA_MAX_GRID)) return LA_EINVAL;
         batch.run_begin[batch.count] = runs;
         const int rc = dispatch_triple<MultiLauncher>(p_dtype, g_dtype, s_dtype, batch, runs + batch.count, st);
         std::memset(&batch, 0, sizeof(batch));
@@ -1426,8 +1433,9 @@ try {
         if (a.n == 0) continue;
         const uint64_t seg_runs = (a.nvec + 63) / 64;
         const uint64_t nscalar = a.head + (a.n - (a.head + a.nvec * kVec));
-        if (nscalar > kMaxSegScalars || seg_runs >= LA_MULTI_OWN_LAUNCH_RUNS) {
-            // pointers out of phase (all elements scalar) or a large segment: its own launch
+        if (nscalar > kMaxSegScalars || seg_runs > LA_MAX_GRID / 2) {
+            // pointers out of phase (all elements scalar), or more runs than one
+            // batch holds: its own launch, which grid-strides
             const int rc = dispatch_triple<StepLauncher>(p_dtype, g_dtype, s_dtype, a, st);
             if (rc != LA_OK) return rc;
             continue;
@@ -1478,8 +1486,20 @@ try {
     if (!coef) return LA_EINVAL;
     // stage 1 writes one partial per workgroup into the fixed array
     if (norm_workspace_bytes(n) > kScratchBytes) return LA_ERANGE;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_rc(e);
+    // the scratch address is the current device's: a stream of another device
+    // would run the kernels there, on that device's memory
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (st != nullptr && st != hipStreamPerThread) {
+        hipDevice_t stream_dev = -1;
+        e = hipStreamGetDevice(st, &stream_dev);
+        if (e != hipSuccess) return hip_rc(e);
+        if (stream_dev != dev) return LA_EINVAL;
+    }
     double* ptr = nullptr;
-    const int rc = scratch_on_current_device(&ptr);
+    const int rc = scratch_on_current_device(dev, &ptr);
     if (rc != LA_OK) return rc;
     return launch_norm(g_dtype, g, n, ptr, kScratchBytes, sqnorm, accumulate, max_norm, coef, norm_out,
                        static_cast<hipStream_t>(stream));

@@ -56,3 +56,33 @@ def test_committed_traffic_profile_is_read():
     value, source = bench.read_traffic()
     assert value == pytest.approx(28 * sum(bench.LLAMA8B_LAYER), rel=1e-4)
     assert "kernel build" in source
+
+
+@pytest.mark.parametrize("env", [{"ROCP_TOOL_LIBRARIES": "x"}, {"ROCPROF_OUTPUT_PATH": "/tmp/la_prof"},
+                                 {"LD_PRELOAD": "librocprofiler-sdk-tool.so"}])
+def test_profiler_environment_is_detected(env, monkeypatch):
+    for k in ("ROCP_TOOL_LIBRARIES", "ROCPROF_OUTPUT_PATH", "LD_PRELOAD"):
+        monkeypatch.delenv(k, raising=False)
+    assert not bench.under_profiler()
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    assert bench.under_profiler()
+
+
+def test_default_run_under_a_profiler_reaches_the_device_check():
+    """`rocprofv3 ... -- python3 bench.py` with the default --traffic live: the
+    run skips its own counter passes and goes on to the device.  Here, on a
+    host without a GPU, it must end at the device check (rc 1), not with a
+    traceback.  The profiler is marked by ROCPROF_OUTPUT_PATH, which only the
+    profiler's own tool reads: a ROCP_TOOL_LIBRARIES naming no library makes
+    the ROCm runtime abort when torch starts it."""
+    import torch
+
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible: this checks the path up to the device check on a host without one")
+    env = dict(os.environ, ROCPROF_OUTPUT_PATH="/tmp/la_prof_unused")
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--steps", "1", "--cpu-budget", "0"],
+                       capture_output=True, text=True, env=env, timeout=300)
+    assert "Traceback" not in r.stderr, r.stderr
+    assert r.returncode == 1 and "needs a HIP device" in r.stderr, (r.returncode, r.stderr)
+    assert "running under a profiler" in r.stderr and r.stdout == ""

@@ -126,3 +126,19 @@ def test_create_and_destroy_on_the_host_registry():
 def test_layer_adam_holds_the_module_as_cpu_adam():
     from slideformer_amd import LayerAdam
     assert LayerAdam().cpu_adam is C
+
+
+def test_creation_log_text_and_stream(capfd):
+    """create_adam(..., should_log=True) prints the reference's two lines
+    (cpu_adam_impl.cpp:116-125) with this build's capability name, on stderr
+    rather than the reference's stdout, so that a caller's stdout (bench.py's
+    one JSON line) stays its own; should_log=False prints nothing."""
+    C.create_adam(77, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, True)
+    C.destroy_adam(77)
+    out, err = capfd.readouterr()
+    assert out == ""
+    assert err == ("Adam Optimizer #77 is created with MI355X (gfx950 HIP) arithmetic capability.\n"
+                   "Config: alpha=0.001000, betas=(0.900000, 0.999000), weight_decay=0.010000, adam_w=1\n")
+    C.create_adam(78, 1e-3, 0.9, 0.999, 1e-8, 0.0, False, False)
+    C.destroy_adam(78)
+    assert capfd.readouterr() == ("", "")

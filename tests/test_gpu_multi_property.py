@@ -11,9 +11,10 @@ skipped steps occur) with their own hyper-parameters, and 1-40 tensors
 elements, each of its streams sits at its own element offset inside its
 buffer (phases that agree or not), and it has a bf16 copy or none; each call
 has a clip coefficient or none.  Half the examples run on the small-grid
-test build of the library, where tensors of 2048 elements or more take their
-own launch and the update kernel's grid-stride loop runs (the product build
-batches tensors of any size and strides only above 2^34 elements).  Every
+test build of the library (64 waves per launch at most), where a batch holds
+at most 32 runs, tensors of more than 32 runs (8192 elements) take their own
+grid-stride launch, and the update kernel's grid-stride loop runs (the product
+build splits batches and strides only above 2^33 elements).  Every
 bit of every tensor's p, m, v and copy must equal the CPU checker replaying
 the same calls one tensor at a time, NaN as a class.  Examples are drawn
 from a fixed seed."""

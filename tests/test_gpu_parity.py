@@ -575,8 +575,9 @@ def test_multi_update_equals_separate_calls(triple, mode, hip_device):
 # ---------------------------------------------------------------------------
 # launch paths the product build takes only at sizes beyond one GPU: the
 # small-grid test build (64 waves per update launch, 2 workgroups per norm
-# launch, own launches from 8 runs per segment, which the product build never
-# gives a segment whose pointers agree in phase) against the product build
+# launch, so at most 32 runs per multi batch and an own grid-stride launch for
+# a segment of more runs, which the product build gives a segment whose
+# pointers agree in phase only above 2^33 elements) against the product build
 # ---------------------------------------------------------------------------
 
 SMALL_GRID_SIZES = [7, 16, 64 * 256 * 3 + 5, 64 * 256 * 40 + 13, 1_000_003]
@@ -587,8 +588,10 @@ def test_grid_stride_update_equals_one_shot(triple, hip_device):
     """The update kernel's grid-stride loop (several trips of 64 waves) and its
     scalar head/tail loop, in the small-grid build, give the same bits as the
     product build's one-shot grid, with a bf16 copy and a clip coefficient,
-    over three steps; the multi-segment entry point likewise, with every
-    segment of 2048 or more elements on its own grid-stride launch.  The
+    over three steps; the multi-segment entry point likewise, where every
+    segment of more than 32 runs (8192 elements: more than one batch of the
+    small-grid build holds) takes its own grid-stride launch and the small
+    ones share batches.  The
     product build is itself pinned to the oracle by the tests above; the
     small-grid results are also checked against the oracle here."""
     pk, gk, sk = triple

@@ -103,3 +103,33 @@ def test_no_alloc_norm_on_a_side_stream_and_empty_input(hip_device):
     # coef is required
     assert L.la_grad_norm_clip_noalloc(_lib.LA_BF16, g.data_ptr(), g.numel(), zero.data_ptr(), 0, 1.0,
                                        None, None, None) == _lib.LA_EINVAL
+
+
+def test_no_alloc_norm_checks_the_stream_device(hip_device):
+    """The fixed array's address is the current device's, so the stream must
+    belong to the current device: the default stream (NULL), the per-thread
+    default stream and a stream created on the current device are accepted,
+    with the same bits as the workspace call; a stream of another device is
+    refused with LA_EINVAL before any launch (needs a second GPU)."""
+    L = _lib.load()
+    g = _grads(1_000_003, torch.bfloat16, hip_device, 23)
+    zero = torch.zeros(1, dtype=torch.float64, device=hip_device)
+    ref = _with_workspace(L, g, 0, zero, 1.0, torch.cuda.current_stream(hip_device).cuda_stream)
+    own = torch.cuda.Stream(hip_device)
+    for name, st in (("NULL", None), ("per-thread", ctypes.c_void_p(2)), ("created", own.cuda_stream)):
+        print(f"no-alloc norm on the {name} stream", flush=True)
+        got = _no_alloc(L, g, 0, zero, 1.0, st)
+        for a, b in zip(got, ref):
+            assert np.array_equal(_bits(a), _bits(b)), name
+    if torch.cuda.device_count() < 2:
+        return
+    other = torch.device("cuda", (hip_device.index + 1) % torch.cuda.device_count())
+    foreign = torch.cuda.Stream(other)
+    sq = zero.clone()
+    coef = torch.full((1,), -1.0, device=hip_device)
+    torch.cuda.synchronize()
+    rc = L.la_grad_norm_clip_noalloc(_lib.LA_BF16, g.data_ptr(), g.numel(), sq.data_ptr(), 0, 1.0,
+                                     coef.data_ptr(), None, foreign.cuda_stream)
+    assert rc == _lib.LA_EINVAL
+    torch.cuda.synchronize()
+    assert coef.item() == -1.0 and sq.item() == 0.0
