@@ -4,8 +4,8 @@ Runs LayerAdam on one GPU under whatever torch caching-allocator
 configuration the parent put into PYTORCH_HIP_ALLOC_CONF (expandable
 segments, the stream-ordered hipMallocAsync backend, or the default), so that
 every device array the library sees comes from that allocator:
-  A. clip_grad_norm over three device grads, then step(layer) twice with the
-     clip coefficient (la_grad_norm_multi, la_adam_update_multi);
+  A. clip_grad_norm over three device grads, then step_with_grad_views twice
+     with the clip coefficient (la_grad_norm_multi, la_adam_update_multi);
   B. step_chunk on flat device buffers with the bf16 copy (la_adam_update);
   C. step_chunk on a host-resident master with device grads and moments
      (la_pipeline_step: its device slots come from the allocator too).
@@ -49,13 +49,13 @@ def main() -> int:
     k = int(inp["a_count"])
     params = [torch.nn.Parameter(f32(inp[f"a_p{i}"])) for i in range(k)]
     grads = [bf16(inp[f"a_g{i}"]) for i in range(k)]
-    for prm, g in zip(params, grads):
-        prm.grad = g
     adam = LayerAdam(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
     adam.add_layer_params(0, params)
     coef, norm = adam.clip_grad_norm(grads, 0.5)
     for _ in range(2):
-        adam.step(0, clip_coef=coef)
+        # bf16 grads of fp32 params, as the runtime hands them over (a param's
+        # .grad must have the param's dtype)
+        adam.step_with_grad_views(0, dict(zip(params, grads)), clip_coef=coef)
     torch.cuda.synchronize()
     out["a_coef"], out["a_norm"] = bits(coef), bits(norm)
     for i, prm in enumerate(params):

@@ -8,7 +8,7 @@ segments (virtual address ranges mapped onto physical pieces,
 hipMemCreate/hipMemMap), and the stream-ordered hipMallocAsync backend.  The
 reference's launch scripts name both of the latter as options.  Each
 configuration runs tests/alloc_child.py in a fresh process: a clipped
-step(layer) of three tensors (twice), a flat step_chunk with the bf16 copy,
+step_with_grad_views of three tensors (twice), a flat step_chunk with the bf16 copy,
 and a streamed step_chunk on a host-resident master with device grads and
 moments.  Every result must equal the CPU checker's bit for bit, and so the
 other configurations' too."""
@@ -28,7 +28,10 @@ pytestmark = pytest.mark.gpu
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CHILD = os.path.join(REPO, "tests", "alloc_child.py")
 CONFIGS = [("default", None, "native"), ("expandable_segments", "expandable_segments:True", "native"),
-           ("hipMallocAsync", "backend:hipMallocAsync", "cudaMallocAsync")]
+           # the ROCm build of torch names this backend "cudaMallocAsync" (and runs
+           # hipMallocAsync under it); "backend:hipMallocAsync" parses at import but is
+           # refused at the first allocation as a mismatch with that name
+           ("hipMallocAsync", "backend:cudaMallocAsync", "cudaMallocAsync")]
 A_SIZES = [10_007, 4096, 333]
 LR, BETAS, EPS, WD = 1e-3, (0.9, 0.999), 1e-8, 0.01
 
