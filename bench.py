@@ -539,6 +539,99 @@ def copy_ceiling(args):
     print(json.dumps(res), flush=True)
 
 
+def update_ceiling(args):
+    """The update kernel's own memory ceiling, in one process on the C2 shape:
+    la_adamw_kernel<float, bf16_t, float> (with a clip coefficient, as in the
+    headline step) beside three probe kernels (libslideformer_amd_probe.so,
+    csrc/stream_probe.hip) that keep its memory side exactly (streams,
+    descriptors, access widths, cache-policy bits, wave priority window, one
+    run per wave, the LDS residency cap) and drop the AdamW arithmetic:
+      copy   the same 28 B/param, values passed through;
+      read   the loads alone, 14 B/param;
+      write  the stores alone, 14 B/param.
+    Each launch is timed with HIP events on its stream, --steps launches per
+    variant and round, in --rounds interleaved rounds; before each launch a
+    plain in-place pass over 1 GiB of other memory leaves none of the
+    launch's inputs in the 256 MB MALL.  --probe-lds lists the LDS
+    reservations (waves per CU = 160 KiB / reservation) to time the probes
+    at; the update keeps its own (13 KiB, 12 waves)."""
+    import ctypes
+
+    import torch
+
+    from slideformer_amd import LayerAdam
+    from slideformer_amd.build import PROBE_LIB
+
+    if not os.path.exists(PROBE_LIB):
+        print(f"{PROBE_LIB} not built: run `python -m slideformer_amd.build`", file=sys.stderr)
+        sys.exit(1)
+    lib = ctypes.CDLL(PROBE_LIB)
+    P = ctypes.c_void_p
+    lib.la_probe_stream.argtypes = [ctypes.c_int, P, P, P, P, P, ctypes.c_uint64, ctypes.c_uint32, P]
+    lib.la_probe_stream.restype = ctypes.c_int
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = sum(LLAMA8B_LAYER)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20)
+    p = torch.randn(n, generator=gen, device=dev) * 0.02
+    m = torch.randn(n, generator=gen, device=dev) * 1e-4
+    v = (torch.randn(n, generator=gen, device=dev) * 1e-4).square_()
+    g = (torch.randn(n, generator=gen, device=dev) * 1e-3).bfloat16()
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    coef = torch.tensor([0.5], device=dev)
+    flush = torch.zeros(256 * 1024 * 1024, device=dev)
+    adam = LayerAdam(lr=1e-5, weight_decay=0.01)
+    stream = torch.cuda.current_stream(dev)
+    step = [0]
+    ldss = [int(x) for x in args.probe_lds.split(",")] if args.probe_lds else [13312]
+
+    def update():
+        step[0] += 1
+        adam.step_chunk(p, g, m, v, dict(adam.defaults, step=step[0]), bf16_out=out, clip_coef=coef,
+                        stream=stream)
+
+    def probe(mode, lds):
+        def run():
+            rc = lib.la_probe_stream(mode, p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                     n, lds, stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"la_probe_stream({mode}) failed: {rc}")
+        return run
+
+    variants = [("update", 28, update)]
+    for lds in ldss:
+        for mode, name, bpp in ((0, "copy", 28), (1, "read", 14), (2, "write", 14)):
+            variants.append((f"{name}@{lds}", bpp, probe(mode, lds)))
+    times = {name: [] for name, _, _ in variants}
+    for fn in [v[2] for v in variants]:
+        fn()
+    torch.cuda.synchronize()
+    for r in range(args.rounds):
+        for name, _, fn in variants:
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            for a, b in evs:
+                flush.add_(1.0)
+                a.record(stream)
+                fn()
+                b.record(stream)
+            torch.cuda.synchronize()
+            times[name] += [a.elapsed_time(b) for a, b in evs]
+        log(f"round {r + 1}/{args.rounds}: " + ", ".join(f"{k} {sum(t) / len(t):.4f} ms" for k, t in times.items()))
+    rows = {}
+    for name, bpp, _ in variants:
+        t = sorted(times[name])
+        avg = sum(t) / len(t)
+        rows[name] = {"ms": round(avg, 4), "ms_min": round(t[0], 4), "ms_median": round(t[len(t) // 2], 4),
+                      "bytes_per_param": bpp, "gbs": round(bpp * n / (avg * 1e-3) / 1e9, 1),
+                      "frac": round(bpp * n / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    print(json.dumps({"metric": "update kernel memory ceiling, C2 shape (probe kernels with its memory side)",
+                      "params": n, "steps": args.steps, "rounds": args.rounds,
+                      "mall": "flushed before each launch (1 GiB in-place pass over other memory)",
+                      "results": rows}), flush=True)
+
+
 def triples(args):
     """The update kernel on every dtype triple the reference registers
     (cpu_adam_impl.cpp:181-189), at the C2 shape (218,112,000 elements), with
@@ -1057,6 +1150,14 @@ def main():
                     help="time the update kernel on every registered dtype triple at the C2 shape")
     ap.add_argument("--triple-filter", default="",
                     help="with --triples: only these triples, e.g. bf16/bf16/bf16,f16/f16/f16")
+    ap.add_argument("--update-ceiling", action="store_true",
+                    help="time the update kernel beside probe kernels with its exact memory side and no "
+                         "arithmetic (pass-through copy, loads only, stores only), C2 shape")
+    ap.add_argument("--probe-lds", default="",
+                    help="with --update-ceiling: comma-separated LDS bytes reserved per probe workgroup "
+                         "(default 13312, the update's: 12 waves per CU)")
+    ap.add_argument("--rounds", type=int, default=3,
+                    help="with --update-ceiling: interleaved rounds of --steps launches per variant")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain HBM copies of one C2 update's bytes beside the update kernel")
     ap.add_argument("--moments-in-hbm", action="store_true",
@@ -1100,7 +1201,8 @@ def main():
 
     # the traffic passes run as child processes before this process touches the GPU
     live = (None, "not measured for this workload")
-    if (args.traffic == "live" and not (args.streamed or args.step_api or args.copy_ceiling or args.triples)
+    if (args.traffic == "live" and not (args.streamed or args.step_api or args.copy_ceiling or args.triples
+                                        or args.update_ceiling)
             and args.config == "c2" and args.shard == 1 and not args.no_clip):
         if under_profiler():
             # no profiler runs of our own under another one: the committed profile serves
@@ -1125,6 +1227,9 @@ def main():
         return
     if args.copy_ceiling:
         copy_ceiling(args)
+        return
+    if args.update_ceiling:
+        update_ceiling(args)
         return
     if args.triples:
         triples(args)

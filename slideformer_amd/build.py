@@ -1,8 +1,9 @@
 """Build recipe for the in-tree HIP library ``slideformer_amd/lib/libslideformer_amd.so``.
 
 Usage: ``python -m slideformer_amd.build`` (also called by ``__graft_entry__.build()``);
-it also writes the small-grid test build ``lib/libslideformer_amd_smallgrid.so`` and the
-C test driver ``tests/native/_build/device_from_c``.
+it also writes the small-grid test build ``lib/libslideformer_amd_smallgrid.so``, the
+stream-probe library ``lib/libslideformer_amd_probe.so`` (bench only) and the C test
+driver ``tests/native/_build/device_from_c``.
 
 The library is one HIP translation unit compiled for gfx950 only.  Flags:
   -ffp-contract=off       every FMA in the kernels is an explicit fmaf(), so the
@@ -48,14 +49,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP library cannot be built")
 
 
-def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: bool = False) -> str:
+def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: bool = False,
+                  sources: list | None = None) -> str:
     """Compile the library for gfx950 into ``out`` (atomically replaced)."""
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
     cmd = [hipcc(), *BASE_FLAGS]
     for k, v in (defines or {}).items():
         cmd.append(f"-D{k}={v}")
-    cmd += ["-I", os.path.join(REPO_DIR, "include"), "-o", tmp, *SOURCES]
+    cmd += ["-I", os.path.join(REPO_DIR, "include"), "-o", tmp, *(sources or SOURCES)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -75,6 +77,14 @@ def build_library(out: str = LIB_PATH, defines: dict | None = None, verbose: boo
 # launch limits differ.
 SMALL_GRID_LIB = os.path.join(LIB_DIR, "libslideformer_amd_smallgrid.so")
 SMALL_GRID_DEFINES = {"LA_MAX_GRID": 64, "LA_NORM_MAX_GRID": 2}
+
+
+# The update kernel's memory-ceiling probes (csrc/stream_probe.hip: its exact
+# memory side with the arithmetic removed), loaded only by
+# `bench.py --update-ceiling`; a library of their own, so that the product
+# library holds no measurement-only kernels.
+PROBE_LIB = os.path.join(LIB_DIR, "libslideformer_amd_probe.so")
+PROBE_SOURCES = [os.path.join(CSRC, "stream_probe.hip")]
 
 
 # A plain C program that runs the step on the GPU through the C-ABI alone
@@ -106,9 +116,10 @@ def build_c_driver(verbose: bool = False) -> str:
 
 
 def build_all(verbose: bool = False) -> list:
-    """The product library, the small-grid test build and the C test driver."""
+    """The product library, the small-grid test build, the stream probes and the C test driver."""
     return [build_library(verbose=verbose),
             build_library(out=SMALL_GRID_LIB, defines=SMALL_GRID_DEFINES, verbose=verbose),
+            build_library(out=PROBE_LIB, sources=PROBE_SOURCES, verbose=verbose),
             build_c_driver(verbose=verbose)]
 
 
