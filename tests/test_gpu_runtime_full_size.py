@@ -1,0 +1,294 @@
+"""The runtime's host-state layouts at full size, bit for bit.
+
+SlideFormer's runtime keeps every layer's fp32 master in pageable host memory
+(transformer_layer.py:192-196), lands each layer's bf16 grads in ONE
+page-locked buffer shared by all layers (:206), copies them there in 32 Mi-
+element chunks with an event per chunk (:26-27, :384-389), and lets an update
+thread call LayerAdam.step_chunk once per chunk on the host master and the
+moments (:453-493).  The smaller tests replay that protocol at a few thousand
+elements; here it runs on a whole Llama-3.1-8B decoder layer, and the whole
+Llama-3.1-8B-shaped model is stepped from host masters in sliding order.
+
+Each streamed result is compared with the same calls on HBM-resident copies
+(every bit of every array), and windows at every call boundary and at the
+ends with the CPU checker replaying the same calls."""
+from __future__ import annotations
+
+import queue
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from slideformer_amd import LayerAdam, _lib
+from tests import _hip as H
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 128256
+LLAMA8B_LAYER = sum([4096 * 4096, 1024 * 4096, 1024 * 4096, 4096 * 4096, 14336 * 4096, 14336 * 4096,
+                     4096 * 14336, 4096, 4096])
+CALL_CHUNK = 32 * 1024 * 1024      # the runtime's chunk, transformer_layer.py:26-27
+PIPE_CHUNK = 16 * 1024 * 1024      # LayerAdam's pipeline chunk for host arrays
+LR, WD = 1e-5, 0.01
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def device_randn(n, seed, dev, std):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    return torch.randn(n, generator=gen, device=dev) * std
+
+
+def equal_on_device(a, b, piece=256 * 1024 * 1024):
+    """Bitwise equality of two equal-sized arrays (either may be in host memory), compared on the device."""
+    dev = b.device if b.is_cuda else a.device
+    iv = torch.int32 if a.element_size() == 4 else torch.int16
+    for lo in range(0, a.numel(), piece):
+        hi = min(a.numel(), lo + piece)
+        if not torch.equal(a[lo:hi].to(dev).view(iv), b[lo:hi].to(dev).view(iv)):
+            return False
+    return True
+
+
+class WindowChecker:
+    """The CPU checker on windows of one optimizer id's buffers.  Each call of
+    the optimizer (one per chunk) is replayed as one checker call on the
+    window pieces that fall inside that chunk, concatenated: every chunk is a
+    multiple of 16 elements and so is every piece, so no piece meets the
+    reference's scalar tail, and the beta-power state advances once per call,
+    as on the device."""
+
+    def __init__(self, windows, p0, m0=None, v0=None):
+        """p0, m0, v0: the initial fp32 arrays (host or device tensors; m0 and
+        v0 None for zeros); only their windows are read."""
+        def win(t, lo, hi):
+            return (np.zeros(hi - lo, np.float32) if t is None
+                    else H.to_np_bits(t[lo:hi], "f32").view(np.float32).copy())
+        self.windows = windows
+        self.p = [win(p0, lo, hi) for lo, hi in windows]
+        self.m = [win(m0, lo, hi) for lo, hi in windows]
+        self.v = [win(v0, lo, hi) for lo, hi in windows]
+        self.orc = O.OracleAdam(LR, (0.9, 0.999), 1e-8, WD, True)
+
+    def call(self, step, cs, ce, g_dev, coef):
+        pieces = []
+        for k, (lo, hi) in enumerate(self.windows):
+            a, b = max(lo, cs), min(hi, ce)
+            if a < b:
+                assert (a - lo) % 16 == 0 and (b - a) % 16 == 0
+                pieces.append((k, a - lo, b - lo, a, b))
+        cat = lambda arrs: (np.concatenate([arrs[k][x:y] for k, x, y, _, _ in pieces]) if pieces  # noqa: E731
+                            else np.zeros(0, np.float32))
+        p, m, v = cat(self.p), cat(self.m), cat(self.v)
+        g = (np.concatenate([H.to_np_bits(g_dev[a:b], "bf16") for _, _, _, a, b in pieces]) if pieces
+             else np.zeros(0, np.uint16))
+        self.orc.update(step, LR, 0.9, 0.999, 1e-8, WD, True, p, g, m, v, g16="bf16", clip_coef=coef)
+        off = 0
+        for k, x, y, _, _ in pieces:
+            self.p[k][x:y], self.m[k][x:y], self.v[k][x:y] = p[off:off + y - x], m[off:off + y - x], v[off:off + y - x]
+            off += y - x
+
+    def check(self, p, m, v, out, what):
+        for k, (lo, hi) in enumerate(self.windows):
+            assert np.array_equal(H.to_np_bits(p[lo:hi], "f32"), self.p[k].view(np.uint32)), (what, "p", lo)
+            assert np.array_equal(H.to_np_bits(m[lo:hi], "f32"), self.m[k].view(np.uint32)), (what, "m", lo)
+            assert np.array_equal(H.to_np_bits(v[lo:hi], "f32"), self.v[k].view(np.uint32)), (what, "v", lo)
+            assert np.array_equal(H.to_np_bits(out[lo:hi], "bf16"), O.f32_to_bf16(self.p[k])), (what, "out", lo)
+
+
+@pytest.mark.parametrize("moments_in_hbm", [False, True])
+def test_runtime_protocol_on_a_full_c2_layer(moments_in_hbm, hip_device):
+    """One Llama-3.1-8B decoder layer (218,112,000 params) through the runtime's
+    host-side protocol, two steps: pageable fp32 master; one page-locked bf16
+    grad buffer that a producer stream fills in 32 Mi-element chunks with an
+    event per chunk; an update thread that waits for each event and calls
+    step_chunk on that chunk of the master, the shared grad buffer and the
+    moments (7 calls per step, the last one short), with
+    overlap_host_chunks=True, the step's clip coefficient and the bf16 copy
+    written into a device cache-unit buffer; then end_chunk_step.  The
+    moments are pageable host arrays (the reference's allocation) or in HBM
+    (moments_device).  Every bit of master, moments and copy equals the same
+    chunk calls on HBM-resident copies, and windows at the start, at every
+    call boundary, at the first pipeline-chunk boundary and at the end equal
+    the CPU checker's."""
+    dev, n = hip_device, LLAMA8B_LAYER
+    seed = 7100 + 10 * int(moments_in_hbm)
+    p0 = device_randn(n, seed, dev, 0.02)
+    master = torch.empty(n, dtype=torch.float32)          # pageable, as the runtime allocates it
+    master.copy_(p0)
+    assert not _lib.is_page_locked(master)
+    adam = LayerAdam(lr=LR, weight_decay=WD, overlap_host_chunks=True,
+                     moments_device=dev if moments_in_hbm else None)
+    adam.add_layer_params(0, [torch.nn.Parameter(master)])
+    m_s, v_s = adam.exp_avg_flat[0], adam.exp_avg_sq_flat[0]
+    assert m_s.is_cuda == moments_in_hbm and (moments_in_hbm or not _lib.is_page_locked(m_s))
+    resident = LayerAdam(lr=LR, weight_decay=WD)
+    p_r = p0.clone()
+    resident.add_layer_params(0, [torch.nn.Parameter(p_r)])
+    m_r, v_r = resident.exp_avg_flat[0], resident.exp_avg_sq_flat[0]
+    shared_grad = torch.empty(n, dtype=torch.bfloat16, pin_memory=True)   # transformer_layer.py:206
+    cache_unit = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    out_r = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    producer = torch.cuda.Stream(device=dev)
+    bounds = list(range(0, n, CALL_CHUNK))
+    assert len(bounds) == 7 and n % CALL_CHUNK != 0 and n % 16 == 0
+    windows = ([(0, 4096), (PIPE_CHUNK - 2048, PIPE_CHUNK + 2048)] + [(b - 2048, b + 2048) for b in bounds[1:]]
+               + [(n - 4096, n)])
+    chk = WindowChecker(windows, p0)
+    del p0
+    for step in (1, 2):
+        g = device_randn(n, seed + step, dev, 1e-3).bfloat16()
+        coef, _ = adam.clip_grad_norm([g], 1.0)
+        torch.cuda.synchronize()
+        c = float(coef.item())
+        assert 0.0 < c < 1.0
+        log(f"C2 protocol (moments {'HBM' if moments_in_hbm else 'host'}): step {step}, coef {c}")
+        q: "queue.Queue" = queue.Queue()
+        errors = []
+
+        def update_thread():
+            try:
+                group = adam.begin_chunk_step(0)
+                while True:
+                    item = q.get()
+                    if item is None:
+                        break
+                    cs, ce, ev = item
+                    ev.synchronize()
+                    adam.step_chunk(master[cs:ce], shared_grad[cs:ce], m_s[cs:ce], v_s[cs:ce], group,
+                                    bf16_out=cache_unit[cs:ce], clip_coef=coef)
+                adam.end_chunk_step(0)
+            except Exception as exc:           # reported by the main thread
+                errors.append(exc)
+
+        t = threading.Thread(target=update_thread)
+        t.start()
+        with torch.cuda.stream(producer):
+            for cs in bounds:
+                ce = min(cs + CALL_CHUNK, n)
+                shared_grad[cs:ce].copy_(g[cs:ce], non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(producer)
+                q.put((cs, ce, ev))
+        q.put(None)
+        t.join(timeout=240)
+        assert not t.is_alive() and not errors, errors
+        group_r = resident.begin_chunk_step(0)
+        for cs in bounds:
+            ce = min(cs + CALL_CHUNK, n)
+            resident.step_chunk(p_r[cs:ce], g[cs:ce], m_r[cs:ce], v_r[cs:ce], group_r, bf16_out=out_r[cs:ce],
+                                clip_coef=coef)
+            chk.call(step, cs, ce, g, c)
+        resident.end_chunk_step(0)
+        torch.cuda.synchronize()
+        log(f"C2 protocol: compare step {step}")
+        for a, b, what in ((master, p_r, "p"), (m_s, m_r, "m"), (v_s, v_r, "v"), (cache_unit, out_r, "out")):
+            assert equal_on_device(a, b), (step, what)
+        chk.check(master, m_s, v_s, cache_unit, f"step {step}")
+        del g, coef
+
+
+@pytest.mark.parametrize("layout", ["moments_in_hbm", "all_on_host"])
+def test_c3_whole_model_streamed_from_host_state(layout, hip_device):
+    """Config C3 stepped whole from host state, in two layouts:
+    - moments_in_hbm, the layout recommended for the runtime: every segment's
+      fp32 master in host memory, its moments in HBM
+      (LayerAdam(moments_device=...)); the masters of lm_head and layers
+      31-16 (sliding order) page-locked at exact size, the other 17 segments
+      pageable and staged;
+    - all_on_host, the reference's own layout: master, m and v of every
+      segment in host memory; those of lm_head and layers 31-12 page-locked
+      at exact size (54.6 GiB: one process may page-lock at most 64 GiB on
+      these hosts), the other 13 segments pageable and staged.
+    bf16 grads and copies in HBM; the moments start from non-zero values.  One
+    step: the global grad norm over all 34 segments in sliding order, one
+    clip coefficient, then every segment stepped in sliding order (lm_head,
+    L31 ... L0, embed; offload_transformer.py:265-301,
+    transformer_layer.py:453-493).  Each segment's master, moments and copy
+    equal, bit for bit, the same calls on HBM-resident copies; windows in
+    both vocab segments and in the first and last decoder layers (start,
+    first pipeline-chunk boundary, end) equal the CPU checker's."""
+    dev = hip_device
+    sizes = [VOCAB * 4096] + [LLAMA8B_LAYER] * 32 + [4096 + VOCAB * 4096]
+    assert sum(sizes) == 8_030_261_248 and len(sizes) == 34
+    order = list(range(33, -1, -1))
+    host_moments = layout == "all_on_host"
+    # lm_head and layers 31-16 (segments 33, 32-17), or 31-12 (33, 32-13)
+    pinned = {33} | set(range(13 if host_moments else 17, 33))
+    assert not host_moments or 12 * sum(sizes[i] for i in pinned) < 55 * 2**30
+    adam = LayerAdam(lr=LR, weight_decay=WD, moments_device=None if host_moments else dev)
+    resident = LayerAdam(lr=LR, weight_decay=WD)
+    masters = []
+    log(f"C3 streamed ({layout}): host state for 34 segments")
+    for idx, n in enumerate(sizes):
+        p0 = device_randn(n, 8000 + idx, dev, 0.02)
+        p_h = _lib.page_locked_empty(n, torch.float32) if idx in pinned else torch.empty(n, dtype=torch.float32)
+        p_h.copy_(p0)
+        masters.append(p_h)
+        adam.pin_host_state = idx in pinned         # read by add_layer_params for host moments
+        assert adam.add_layer_params(idx, [torch.nn.Parameter(p_h)]) == idx
+        adam.exp_avg_flat[idx].copy_(device_randn(n, 9000 + idx, dev, 1e-5))
+        adam.exp_avg_sq_flat[idx].copy_(device_randn(n, 10000 + idx, dev, 3e-5).square_())
+        m_h = adam.exp_avg_flat[idx]
+        assert m_h.is_cuda != host_moments and _lib.is_page_locked(p_h) == (idx in pinned)
+        assert not host_moments or _lib.is_page_locked(m_h) == (idx in pinned)
+        # the resident twin registers an empty stand-in: its state is made per segment at step time
+        assert resident.add_layer_params(idx, [torch.nn.Parameter(torch.empty(1, device=dev))]) == idx
+        del p0
+    torch.cuda.synchronize()
+
+    def grads(idx):
+        return device_randn(sizes[idx], 11000 + idx, dev, 1e-3).bfloat16()
+
+    log(f"C3 streamed ({layout}): global grad norm in sliding order")
+    acc = adam.grad_norm_begin(dev)
+    for idx in order:
+        acc.add(grads(idx))
+    coef, _ = acc.finish(1.0)
+    torch.cuda.synchronize()
+    c = float(coef.item())
+    assert 0.0 < c < 1.0
+
+    checked = {0, 1, 32, 33}                              # embed, layer 0, layer 31, lm_head
+    for j, idx in enumerate(order):
+        n = sizes[idx]
+        g = grads(idx)
+        windows = [(0, 4096), (PIPE_CHUNK - 2048, PIPE_CHUNK + 2048), (n - 4096, n)]
+        # the resident replay of this segment, from the same initial values
+        p_r = device_randn(n, 8000 + idx, dev, 0.02)
+        m_r = adam.exp_avg_flat[idx].to(dev, copy=True)
+        v_r = adam.exp_avg_sq_flat[idx].to(dev, copy=True)
+        chk = WindowChecker(windows, p_r, m_r, v_r) if idx in checked else None
+        out_s = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        out_r = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        group = adam.begin_chunk_step(idx)
+        adam.step_chunk(masters[idx], g, adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], group, bf16_out=out_s,
+                        clip_coef=coef)
+        adam.end_chunk_step(idx)
+        st = adam.last_stream_stats
+        assert st.h2d_bytes == st.d2h_bytes == (12 if host_moments else 4) * n   # the host arrays crossed the link
+        group_r = resident.begin_chunk_step(idx)
+        resident.step_chunk(p_r, g, m_r, v_r, group_r, bf16_out=out_r, clip_coef=coef)
+        resident.end_chunk_step(idx)
+        torch.cuda.synchronize()
+        for a, b, what in ((masters[idx], p_r, "p"), (adam.exp_avg_flat[idx], m_r, "m"),
+                           (adam.exp_avg_sq_flat[idx], v_r, "v"), (out_s, out_r, "out")):
+            assert equal_on_device(a, b), (idx, what)
+        if chk is not None:
+            log(f"C3 streamed ({layout}): segment {idx} (call {j} of the step) against the CPU checker")
+            for _ in range(j):          # the earlier calls of this step on the same optimizer id
+                chk.call(1, 0, 0, g, c)
+            chk.call(1, 0, n, g, c)
+            chk.check(masters[idx], adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], out_s, f"segment {idx}")
+        if j % 8 == 0:
+            log(f"C3 streamed ({layout}): {j + 1} of 34 segments stepped and compared")
+        del g, p_r, m_r, v_r, out_s, out_r
+    del adam, resident, masters, acc
+    torch._C._host_emptyCache()
+    torch.cuda.empty_cache()
