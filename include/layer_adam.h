@@ -236,7 +236,8 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *
  * la_pipeline_create: chunk_elems is rounded down to a multiple of 16 (only
  *   the last chunk of a call then holds the reference's scalar tail); 1..16
- *   staging slots.  Creates the streams and events; allocates no memory.
+ *   staging slots.  Creates the streams and events on the current device,
+ *   which the pipeline then belongs to; allocates no memory.
  * la_pipeline_workspace_bytes: device staging bytes the caller must provide
  *   (256-byte aligned) for the given element types and placement.
  * la_pipeline_step: one reference adam_update over n elements (p, m, v, g
@@ -256,7 +257,9 @@ int la_clip_coef(const double* sqnorm, float max_norm, float* coef, float* norm_
  *   earlier unsettled call, or using another workspace or slot layout
  *   (element types, placement) than the previous call, settles everything
  *   first.  Device-resident arrays are updated in call order on one stream.
- *   One pipeline object must not be used by two threads at once.
+ *   One pipeline object must not be used by two threads at once.  The call
+ *   needs the pipeline's device current (LA_EINVAL otherwise), with the
+ *   workspace and the device-resident arrays on that device.
  * la_pipeline_sync: wait until every queued call is complete in host memory.
  * la_pipeline_set_host_staging: attach caller-owned page-locked host memory
  *   (256-byte aligned, at least la_pipeline_workspace_bytes() for the call's

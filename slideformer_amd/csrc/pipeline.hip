@@ -334,6 +334,14 @@ try {
     if (on_host & ~LA_ON_HOST_ALL) return LA_EINVAL;
     if (n == 0) return LA_OK;
     if (!p || !g || !m || !v || !workspace) return LA_EINVAL;
+    {
+        // the pipeline's streams belong to the device current at creation, and so
+        // must the update it launches there and the device arrays it touches
+        int cur = -1;
+        const hipError_t e = hipGetDevice(&cur);
+        if (e != hipSuccess) return rc_of(e);
+        if (cur != pl->device) return LA_EINVAL;
+    }
     const bool hp = on_host & LA_ON_HOST_P, hm = on_host & LA_ON_HOST_M, hv = on_host & LA_ON_HOST_V;
     const bool hg = on_host & LA_ON_HOST_G, ho = on_host & LA_ON_HOST_OUT;
     if (ho && !out) return LA_EINVAL;

@@ -1242,8 +1242,9 @@ def test_streamed_call_beyond_2_pow_32_elements(hip_device):
 
 
 def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
-    """la_pipeline_step validates the dtype triple and device-pointer alignment
-    up front: the host state is left untouched."""
+    """la_pipeline_step validates the dtype triple, device-pointer alignment,
+    placement and the current device up front: the host state is left
+    untouched."""
     import ctypes
 
     from slideformer_amd import _lib
@@ -1288,6 +1289,10 @@ def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V) == _lib.LA_EFAULT
     mh = torch.zeros(n)
     assert call(g.data_ptr(), on_host=_lib.LA_ON_HOST_P | _lib.LA_ON_HOST_V, mptr=mh.data_ptr()) == _lib.LA_EFAULT
+    # another device current than the pipeline's (needs a second GPU)
+    if torch.cuda.device_count() > 1:
+        with torch.cuda.device((hip_device.index + 1) % torch.cuda.device_count()):
+            assert call(g.data_ptr()) == _lib.LA_EINVAL
     torch.cuda.synchronize()
     assert torch.equal(p, p_before) and not m.any() and not v.any() and not mh.any()
     L.la_destroy(77)
