@@ -10,8 +10,8 @@ elements; here it runs on a whole Llama-3.1-8B decoder layer, and the whole
 Llama-3.1-8B-shaped model is stepped from host masters in sliding order.
 
 Each streamed result is compared with the same calls on HBM-resident copies
-(every bit of every array), and windows at every call boundary and at the
-ends with the CPU checker replaying the same calls."""
+(every bit of every array) and with the CPU checker replaying the same calls:
+over the whole C2 layer, and in windows of the C3 segments."""
 from __future__ import annotations
 
 import queue
@@ -31,7 +31,6 @@ VOCAB = 128256
 LLAMA8B_LAYER = sum([4096 * 4096, 1024 * 4096, 1024 * 4096, 4096 * 4096, 14336 * 4096, 14336 * 4096,
                      4096 * 14336, 4096, 4096])
 CALL_CHUNK = 32 * 1024 * 1024      # the runtime's chunk, transformer_layer.py:26-27
-PIPE_CHUNK = 16 * 1024 * 1024      # LayerAdam's pipeline chunk for host arrays
 LR, WD = 1e-5, 0.01
 
 
@@ -56,50 +55,10 @@ def equal_on_device(a, b, piece=256 * 1024 * 1024):
     return True
 
 
-class WindowChecker:
-    """The CPU checker on windows of one optimizer id's buffers.  Each call of
-    the optimizer (one per chunk) is replayed as one checker call on the
-    window pieces that fall inside that chunk, concatenated: every chunk is a
-    multiple of 16 elements and so is every piece, so no piece meets the
-    reference's scalar tail, and the beta-power state advances once per call,
-    as on the device."""
-
-    def __init__(self, windows, p0, m0=None, v0=None):
-        """p0, m0, v0: the initial fp32 arrays (host or device tensors; m0 and
-        v0 None for zeros); only their windows are read."""
-        def win(t, lo, hi):
-            return (np.zeros(hi - lo, np.float32) if t is None
-                    else H.to_np_bits(t[lo:hi], "f32").view(np.float32).copy())
-        self.windows = windows
-        self.p = [win(p0, lo, hi) for lo, hi in windows]
-        self.m = [win(m0, lo, hi) for lo, hi in windows]
-        self.v = [win(v0, lo, hi) for lo, hi in windows]
-        self.orc = O.OracleAdam(LR, (0.9, 0.999), 1e-8, WD, True)
-
-    def call(self, step, cs, ce, g_dev, coef):
-        pieces = []
-        for k, (lo, hi) in enumerate(self.windows):
-            a, b = max(lo, cs), min(hi, ce)
-            if a < b:
-                assert (a - lo) % 16 == 0 and (b - a) % 16 == 0
-                pieces.append((k, a - lo, b - lo, a, b))
-        cat = lambda arrs: (np.concatenate([arrs[k][x:y] for k, x, y, _, _ in pieces]) if pieces  # noqa: E731
-                            else np.zeros(0, np.float32))
-        p, m, v = cat(self.p), cat(self.m), cat(self.v)
-        g = (np.concatenate([H.to_np_bits(g_dev[a:b], "bf16") for _, _, _, a, b in pieces]) if pieces
-             else np.zeros(0, np.uint16))
-        self.orc.update(step, LR, 0.9, 0.999, 1e-8, WD, True, p, g, m, v, g16="bf16", clip_coef=coef)
-        off = 0
-        for k, x, y, _, _ in pieces:
-            self.p[k][x:y], self.m[k][x:y], self.v[k][x:y] = p[off:off + y - x], m[off:off + y - x], v[off:off + y - x]
-            off += y - x
-
-    def check(self, p, m, v, out, what):
-        for k, (lo, hi) in enumerate(self.windows):
-            assert np.array_equal(H.to_np_bits(p[lo:hi], "f32"), self.p[k].view(np.uint32)), (what, "p", lo)
-            assert np.array_equal(H.to_np_bits(m[lo:hi], "f32"), self.m[k].view(np.uint32)), (what, "m", lo)
-            assert np.array_equal(H.to_np_bits(v[lo:hi], "f32"), self.v[k].view(np.uint32)), (what, "v", lo)
-            assert np.array_equal(H.to_np_bits(out[lo:hi], "bf16"), O.f32_to_bf16(self.p[k])), (what, "out", lo)
+def bits_equal(got, want, kind):
+    """Indices (at most 8) where a tensor's bits differ from a checker array's."""
+    w = want.view(np.uint32) if kind == "f32" else want
+    return np.flatnonzero(H.to_np_bits(got, kind) != w)[:8]
 
 
 @pytest.mark.parametrize("moments_in_hbm", [False, True])
@@ -113,10 +72,9 @@ def test_runtime_protocol_on_a_full_c2_layer(moments_in_hbm, hip_device):
     overlap_host_chunks=True, the step's clip coefficient and the bf16 copy
     written into a device cache-unit buffer; then end_chunk_step.  The
     moments are pageable host arrays (the reference's allocation) or in HBM
-    (moments_device).  Every bit of master, moments and copy equals the same
-    chunk calls on HBM-resident copies, and windows at the start, at every
-    call boundary, at the first pipeline-chunk boundary and at the end equal
-    the CPU checker's."""
+    (moments_device).  After each step, every bit of master, moments and copy
+    equals the CPU checker replaying the same seven calls over the whole
+    layer, and the same calls on HBM-resident copies."""
     dev, n = hip_device, LLAMA8B_LAYER
     seed = 7100 + 10 * int(moments_in_hbm)
     p0 = device_randn(n, seed, dev, 0.02)
@@ -138,9 +96,11 @@ def test_runtime_protocol_on_a_full_c2_layer(moments_in_hbm, hip_device):
     producer = torch.cuda.Stream(device=dev)
     bounds = list(range(0, n, CALL_CHUNK))
     assert len(bounds) == 7 and n % CALL_CHUNK != 0 and n % 16 == 0
-    windows = ([(0, 4096), (PIPE_CHUNK - 2048, PIPE_CHUNK + 2048)] + [(b - 2048, b + 2048) for b in bounds[1:]]
-               + [(n - 4096, n)])
-    chk = WindowChecker(windows, p0)
+    # the CPU checker's copy of the whole layer
+    orc = O.OracleAdam(LR, (0.9, 0.999), 1e-8, WD, True)
+    p_o = H.to_np_bits(p0, "f32").view(np.float32).copy()
+    m_o, v_o = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    out_o = np.zeros(n, np.uint16)
     del p0
     for step in (1, 2):
         g = device_randn(n, seed + step, dev, 1e-3).bfloat16()
@@ -180,18 +140,23 @@ def test_runtime_protocol_on_a_full_c2_layer(moments_in_hbm, hip_device):
         t.join(timeout=240)
         assert not t.is_alive() and not errors, errors
         group_r = resident.begin_chunk_step(0)
+        g_h = H.to_np_bits(g, "bf16")
         for cs in bounds:
             ce = min(cs + CALL_CHUNK, n)
             resident.step_chunk(p_r[cs:ce], g[cs:ce], m_r[cs:ce], v_r[cs:ce], group_r, bf16_out=out_r[cs:ce],
                                 clip_coef=coef)
-            chk.call(step, cs, ce, g, c)
+            orc.update(step, LR, 0.9, 0.999, 1e-8, WD, True, p_o[cs:ce], g_h[cs:ce], m_o[cs:ce], v_o[cs:ce],
+                       g16="bf16", p_bf16_out=out_o[cs:ce], clip_coef=c)
         resident.end_chunk_step(0)
         torch.cuda.synchronize()
-        log(f"C2 protocol: compare step {step}")
+        log(f"C2 protocol: compare step {step} with the resident calls and the CPU checker")
         for a, b, what in ((master, p_r, "p"), (m_s, m_r, "m"), (v_s, v_r, "v"), (cache_unit, out_r, "out")):
             assert equal_on_device(a, b), (step, what)
-        chk.check(master, m_s, v_s, cache_unit, f"step {step}")
-        del g, coef
+        for got, want, kind, what in ((master, p_o, "f32", "p"), (m_s, m_o, "f32", "m"), (v_s, v_o, "f32", "v"),
+                                      (cache_unit, out_o, "bf16", "out")):
+            bad = bits_equal(got, want, kind)
+            assert bad.size == 0, (step, what, bad)
+        del g, g_h, coef
 
 
 @pytest.mark.parametrize("layout", ["moments_in_hbm", "all_on_host"])
@@ -211,9 +176,9 @@ def test_c3_whole_model_streamed_from_host_state(layout, hip_device):
     clip coefficient, then every segment stepped in sliding order (lm_head,
     L31 ... L0, embed; offload_transformer.py:265-301,
     transformer_layer.py:453-493).  Each segment's master, moments and copy
-    equal, bit for bit, the same calls on HBM-resident copies; windows in
-    both vocab segments and in the first and last decoder layers (start,
-    first pipeline-chunk boundary, end) equal the CPU checker's."""
+    equal, bit for bit, the same calls on HBM-resident copies; both vocab
+    segments and the first and last decoder layers also equal, every element,
+    the CPU checker replaying the step's calls on one optimizer id."""
     dev = hip_device
     sizes = [VOCAB * 4096] + [LLAMA8B_LAYER] * 32 + [4096 + VOCAB * 4096]
     assert sum(sizes) == 8_030_261_248 and len(sizes) == 34
@@ -259,12 +224,12 @@ def test_c3_whole_model_streamed_from_host_state(layout, hip_device):
     for j, idx in enumerate(order):
         n = sizes[idx]
         g = grads(idx)
-        windows = [(0, 4096), (PIPE_CHUNK - 2048, PIPE_CHUNK + 2048), (n - 4096, n)]
         # the resident replay of this segment, from the same initial values
         p_r = device_randn(n, 8000 + idx, dev, 0.02)
         m_r = adam.exp_avg_flat[idx].to(dev, copy=True)
         v_r = adam.exp_avg_sq_flat[idx].to(dev, copy=True)
-        chk = WindowChecker(windows, p_r, m_r, v_r) if idx in checked else None
+        if idx in checked:      # the checker's copy of the whole segment
+            p_o, m_o, v_o = (H.to_np_bits(t, "f32").view(np.float32).copy() for t in (p_r, m_r, v_r))
         out_s = torch.empty(n, dtype=torch.bfloat16, device=dev)
         out_r = torch.empty(n, dtype=torch.bfloat16, device=dev)
         group = adam.begin_chunk_step(idx)
@@ -280,12 +245,21 @@ def test_c3_whole_model_streamed_from_host_state(layout, hip_device):
         for a, b, what in ((masters[idx], p_r, "p"), (adam.exp_avg_flat[idx], m_r, "m"),
                            (adam.exp_avg_sq_flat[idx], v_r, "v"), (out_s, out_r, "out")):
             assert equal_on_device(a, b), (idx, what)
-        if chk is not None:
+        if idx in checked:
             log(f"C3 streamed ({layout}): segment {idx} (call {j} of the step) against the CPU checker")
+            orc = O.OracleAdam(LR, (0.9, 0.999), 1e-8, WD, True)
+            e = np.zeros(0, np.float32)
             for _ in range(j):          # the earlier calls of this step on the same optimizer id
-                chk.call(1, 0, 0, g, c)
-            chk.call(1, 0, n, g, c)
-            chk.check(masters[idx], adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], out_s, f"segment {idx}")
+                orc.update(1, LR, 0.9, 0.999, 1e-8, WD, True, e, np.zeros(0, np.uint16), e.copy(), e.copy(),
+                           g16="bf16")
+            out_o = np.zeros(n, np.uint16)
+            orc.update(1, LR, 0.9, 0.999, 1e-8, WD, True, p_o, H.to_np_bits(g, "bf16"), m_o, v_o, g16="bf16",
+                       p_bf16_out=out_o, clip_coef=c)
+            for got, want, kind, what in ((masters[idx], p_o, "f32", "p"), (adam.exp_avg_flat[idx], m_o, "f32", "m"),
+                                          (adam.exp_avg_sq_flat[idx], v_o, "f32", "v"), (out_s, out_o, "bf16", "out")):
+                bad = bits_equal(got, want, kind)
+                assert bad.size == 0, (idx, what, bad)
+            del p_o, m_o, v_o, out_o
         if j % 8 == 0:
             log(f"C3 streamed ({layout}): {j + 1} of 34 segments stepped and compared")
         del g, p_r, m_r, v_r, out_s, out_r
