@@ -1126,9 +1126,9 @@ def test_c5_streamed_full_size_matches_resident(hip_device):
     """Config C5 at full size (1,812,099,072 params, 7.25 GB per fp32 array):
     pinned host state streamed through HBM in 256 MB chunks x 2 slots gives the
     same bits as the same step on HBM-resident copies, with one clip coefficient
-    from the grad norm.  Host byte offsets pass 2^32;
-    windows at the start, across element 2^30 (byte 2^32) and at the end (in
-    the short last chunk) are also checked against the oracle."""
+    from the grad norm.  Host byte offsets pass 2^32.  Every element of the
+    streamed master, moments and copy also equals the CPU checker's step over
+    the whole layer."""
     from slideformer_amd.layer_adam import HostStreamer
 
     n = sum(c5_layer_sizes())
@@ -1140,8 +1140,8 @@ def test_c5_streamed_full_size_matches_resident(hip_device):
     m_d = torch.randn(n, generator=gen, device=hip_device) * 1e-4
     v_d = torch.rand(n, generator=gen, device=hip_device) * 1e-8
     g = (torch.randn(n, generator=gen, device=hip_device) * 5e-4).bfloat16()
-    windows = [(0, 4096), ((1 << 30) - 2048, (1 << 30) + 2048), (n - 4096, n)]
-    init = [[t[lo:hi].cpu().numpy().copy() for t in (p_d, m_d, v_d)] for lo, hi in windows]
+    # the CPU checker's copy of the whole layer
+    p_o, m_o, v_o = (H.to_np_bits(t, "f32").view(np.float32) for t in (p_d, m_d, v_d))
     host = []
     for t in (p_d, m_d, v_d):
         h = torch.empty(n, dtype=torch.float32, pin_memory=True)
@@ -1170,15 +1170,17 @@ def test_c5_streamed_full_size_matches_resident(hip_device):
             hi = min(n, lo + piece)
             assert torch.equal(hst[lo:hi].to(hip_device).view(torch.int32), dev[lo:hi].view(torch.int32)), lo
     assert torch.equal(out_s.view(torch.int16), out_d.view(torch.int16))
-    for (lo, hi), (p0, m0, v0) in zip(windows, init):
-        orc = O.OracleAdam(6e-6, (0.9, 0.999), 1e-8, 0.01, True)
-        orc.update(1, 6e-6, 0.9, 0.999, 1e-8, 0.01, True, p0, H.to_np_bits(g[lo:hi], "bf16"), m0, v0,
-                   g16="bf16", clip_coef=c)
-        assert np.array_equal(p_h[lo:hi].numpy().view(np.uint32), p0.view(np.uint32)), lo
-        assert np.array_equal(m_h[lo:hi].numpy().view(np.uint32), m0.view(np.uint32)), lo
-        assert np.array_equal(v_h[lo:hi].numpy().view(np.uint32), v0.view(np.uint32)), lo
-        assert np.array_equal(H.to_np_bits(out_s[lo:hi], "bf16"), O.f32_to_bf16(p0)), lo
-    del p_h, m_h, v_h, host, p_d, m_d, v_d, g, out_d, out_s
+    print("streamed == resident; the CPU checker over the whole layer", flush=True)
+    out_o = np.zeros(n, np.uint16)
+    orc = O.OracleAdam(6e-6, (0.9, 0.999), 1e-8, 0.01, True)
+    orc.update(1, 6e-6, 0.9, 0.999, 1e-8, 0.01, True, p_o, H.to_np_bits(g, "bf16"), m_o, v_o, g16="bf16",
+               p_bf16_out=out_o, clip_coef=c)
+    for got, want, what in ((p_h, p_o, "p"), (m_h, m_o, "m"), (v_h, v_o, "v")):
+        bad = np.flatnonzero(got.numpy().view(np.uint32) != want.view(np.uint32))[:8]
+        assert bad.size == 0, (what, bad)
+    bad = np.flatnonzero(H.to_np_bits(out_s, "bf16") != out_o)[:8]
+    assert bad.size == 0, ("out", bad)
+    del p_h, m_h, v_h, host, p_d, m_d, v_d, g, out_d, out_s, p_o, m_o, v_o, out_o
     torch._C._host_emptyCache()
     torch.cuda.empty_cache()
 
@@ -1188,8 +1190,8 @@ def test_streamed_call_beyond_2_pow_32_elements(hip_device):
     pageable host memory (17 GB, staged through the page-locked twins) and the
     moments, grads and bf16 copy in HBM: 257 pipeline chunks whose element and
     byte offsets pass 2^32.  Same bits as the step on HBM-resident copies, and
-    windows at the start, across elements 2^31 and 2^32 and at the end (the
-    scalar tail) equal the oracle's."""
+    every element (the 13-element scalar tail included) equals the CPU
+    checker's step over the whole call."""
     from slideformer_amd.layer_adam import HostStreamer
 
     n = (1 << 32) + (1 << 20) + 13
@@ -1200,9 +1202,8 @@ def test_streamed_call_beyond_2_pow_32_elements(hip_device):
     m_d = torch.randn(n, generator=gen, device=hip_device) * 1e-4
     v_d = torch.rand(n, generator=gen, device=hip_device) * 1e-8
     g = (torch.randn(n, generator=gen, device=hip_device) * 1e-3).bfloat16()
-    windows = [(0, 4096), ((1 << 31) - 2048, (1 << 31) + 2048), ((1 << 32) - 2048, (1 << 32) + 2048),
-               (n - 4096 - 13, n)]
-    init = [[t[lo:hi].cpu().numpy().copy() for t in (p_d, m_d, v_d)] for lo, hi in windows]
+    # the CPU checker's copy of the whole call
+    p_o, m_o, v_o = (H.to_np_bits(t, "f32").view(np.float32) for t in (p_d, m_d, v_d))
     p_h = torch.empty(n, dtype=torch.float32)                    # pageable, as the runtime allocates it
     piece = 256 * 1024 * 1024
     for lo in range(0, n, piece):
@@ -1229,15 +1230,19 @@ def test_streamed_call_beyond_2_pow_32_elements(hip_device):
     assert torch.equal(m_s.view(torch.int32), m_d.view(torch.int32))
     assert torch.equal(v_s.view(torch.int32), v_d.view(torch.int32))
     assert torch.equal(out_s.view(torch.int16), out_d.view(torch.int16))
-    for (lo, hi), (p0, m0, v0) in zip(windows, init):
-        orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
-        orc.update(1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p0, H.to_np_bits(g[lo:hi], "bf16"), m0, v0, g16="bf16")
-        assert (hi - lo) % 16 == (n % 16 if hi == n else 0)
-        assert np.array_equal(p_h[lo:hi].numpy().view(np.uint32), p0.view(np.uint32)), lo
-        assert np.array_equal(H.to_np_bits(m_s[lo:hi], "f32"), m0.view(np.uint32)), lo
-        assert np.array_equal(H.to_np_bits(v_s[lo:hi], "f32"), v0.view(np.uint32)), lo
-        assert np.array_equal(H.to_np_bits(out_s[lo:hi], "bf16"), O.f32_to_bf16(p0)), lo
-    del p_h, p_d, m_d, v_d, m_s, v_s, g, out_d, out_s, streamed, resident
+    print("streamed == resident; the CPU checker over the whole call", flush=True)
+    del p_d, m_d, v_d, out_d
+    out_o = np.zeros(n, np.uint16)
+    orc = O.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    orc.update(1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p_o, H.to_np_bits(g, "bf16"), m_o, v_o, g16="bf16",
+               p_bf16_out=out_o)
+    bad = np.flatnonzero(p_h.numpy().view(np.uint32) != p_o.view(np.uint32))[:8]
+    assert bad.size == 0, ("p", bad)
+    for got, want, kind, what in ((m_s, m_o, "f32", "m"), (v_s, v_o, "f32", "v"), (out_s, out_o, "bf16", "out")):
+        w = want.view(np.uint32) if kind == "f32" else want
+        bad = np.flatnonzero(H.to_np_bits(got, kind) != w)[:8]
+        assert bad.size == 0, (what, bad)
+    del p_h, m_s, v_s, g, out_s, streamed, resident, p_o, m_o, v_o, out_o
     torch.cuda.empty_cache()
 
 
