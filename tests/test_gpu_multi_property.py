@@ -23,12 +23,13 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
-from hypothesis import HealthCheck, given, settings
+from hypothesis import given
 from hypothesis import strategies as st
 
 from oracle import oracle as O
 from tests import _golden as G
 from tests import _hip as H
+from tests._props import property_test
 
 pytestmark = pytest.mark.gpu
 
@@ -72,7 +73,7 @@ def cases(draw):
                 steps=draw(st.lists(step(), min_size=1, max_size=3)), seed=draw(st.integers(0, 2**31 - 1)))
 
 
-@settings(max_examples=200, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@property_test(200)
 @given(c=cases())
 def test_multi_update_equals_checker_on_random_layers(c, hip_device):
     print(f"multi property case: {c}", flush=True)

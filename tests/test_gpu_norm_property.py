@@ -22,12 +22,13 @@ import math
 import numpy as np
 import pytest
 import torch
-from hypothesis import HealthCheck, given, settings
+from hypothesis import given
 from hypothesis import strategies as st
 
 from oracle import oracle as O
 from slideformer_amd import _lib
 from tests import _hip as H
+from tests._props import property_test
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +54,7 @@ def _bits(x: np.ndarray, kind: str) -> np.ndarray:
     return H.to_np_bits(torch.from_numpy(x.astype(np.float32)).to(H.TD[kind]), kind)
 
 
-@settings(max_examples=200, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@property_test(200)
 @given(c=cases())
 def test_accumulated_norm_and_clip_equal_checker(c, hip_device):
     print(f"norm property case: {c}", flush=True)

@@ -14,12 +14,13 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
-from hypothesis import HealthCheck, given, settings
+from hypothesis import given
 from hypothesis import strategies as st
 
 from slideformer_amd import LayerAdam
 from slideformer_amd.layer_adam import SUPPORTED_TRIPLES, HostStreamer
 from tests import _hip as H
+from tests._props import property_test
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +50,7 @@ def _place(t, host, pinned, dev):
     return t.pin_memory() if pinned else t.clone()
 
 
-@settings(max_examples=200, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@property_test(200)
 @given(c=cases())
 def test_pipeline_equals_resident_on_random_layouts(c, hip_device):
     print(f"pipeline property case: {c}", flush=True)

@@ -17,12 +17,13 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
-from hypothesis import HealthCheck, given, settings
+from hypothesis import given
 from hypothesis import strategies as st
 
 from oracle import oracle as O
 from tests import _golden as G
 from tests import _hip as H
+from tests._props import property_test
 
 pytestmark = pytest.mark.gpu
 
@@ -69,7 +70,7 @@ def cases(draw):
                 calls=draw(st.lists(call(), min_size=1, max_size=4)), seed=draw(st.integers(0, 2**31 - 1)))
 
 
-@settings(max_examples=500, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@property_test(500)
 @given(c=cases())
 def test_device_update_equals_checker_on_random_calls(c, hip_device):
     print(f"update property case: {c}", flush=True)
