@@ -16,7 +16,17 @@ same run with two rocprofv3 --pmc passes over a short child run (the L2's
 sized read and write requests), before this process touches the GPU.
 ``cpu_baseline`` times the reference CPU Adam (compiled from its own sources
 into oracle/_ref, or the C restatement in oracle/ when that is absent) on this
-host, on the same layer size.
+host, on the same layer size.  ``update_kernel_ms_no_mall`` (and
+``roofline.achieved_no_mall`` / ``frac_no_mall``) time the same update launch
+after the timed steps, with a plain pass over 1 GiB of other memory before
+each launch, so that none of the grads the norm pass read are still in the
+256 MB memory-side cache.
+
+Other modes print their own JSON line: ``--streamed c3-layer|c5|c3`` (state in
+host RAM, with the reference CPU Adam timed in the same run), ``--config
+c3|c4`` (whole resident models), ``--step-api``, ``--triples``,
+``--copy-ceiling``, ``--update-ceiling`` (the update kernel's own memory
+ceiling), ``--shard W`` and ``--disk-bench``.
 """
 from __future__ import annotations
 
