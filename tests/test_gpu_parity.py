@@ -199,8 +199,8 @@ def test_all_16bit_triples_every_head_phase(kind, offsets, hip_device):
     whose lanes own 8 consecutive elements: the head that aligns every stream,
     the bf16 copy included, to 8-element (16-byte) groups, the 512-element
     runs, the remainder and the reference's scalar tail.  Every head phase
-    0-7, phases that agree only modulo 4 (then the whole call takes the scalar
-    path), sizes around 8, 16, 512 and the tail, with the bf16 copy and a clip
+    0-7, phases that agree only modulo 4 (then the call takes la_adamw_kernel's
+    4-element layout), sizes around 8, 16, 512 and the tail, with the bf16 copy and a clip
     coefficient: every bit equals the oracle's."""
     op, og, om, ov, oo = offsets
     log(f"16-bit triple {kind} offsets {offsets}")
