@@ -266,3 +266,71 @@ def test_c3_whole_model_streamed_from_host_state(layout, hip_device):
     del adam, resident, masters, acc
     torch._C._host_emptyCache()
     torch.cuda.empty_cache()
+
+
+C5_LAYER = sum([12288 * 3 * 12288, 3 * 12288, 12288 * 12288, 12288, 12288 * 49152, 49152, 49152 * 12288, 12288,
+                12288, 12288, 12288, 12288])
+
+
+def test_nvme_offload_of_a_c5_layer(hip_device, tmp_path):
+    """The moment file offload at full size (layer_adam.py:92-106, 200-247):
+    a C5 layer (1,812,099,072 params; each moment a 7.25 GB file, so file
+    offsets pass 2^32 bytes) and a small layer, nvme_offload_fraction=1.0,
+    prefetch=True, direct I/O (the reference's backend name 'uring'), two
+    iterations in sliding order (small layer, then C5), the runtime's
+    begin_chunk_step / step_chunk / end_chunk_step with device grads and the
+    master in pageable host memory.  Between the steps the moments live only
+    in their files (storage released).  After the last write-back every
+    element of both masters and of both layers' moments, read back from the
+    files, equals the CPU checker's replay."""
+    dev = hip_device
+    sizes = [C5_LAYER, 10_001]
+    assert sizes[0] == 1_812_099_072
+    adam = LayerAdam(lr=6e-6, weight_decay=0.01, num_layer=2, nvme_offload_fraction=1.0,
+                     offload_dir=str(tmp_path), prefetch=True)
+    assert adam.offloader.direct
+    params, p_o = [], []
+    for idx, n in enumerate(sizes):
+        p0 = device_randn(n, 12000 + idx, dev, 0.02)
+        p_h = torch.empty(n, dtype=torch.float32)
+        p_h.copy_(p0)
+        params.append(torch.nn.Parameter(p_h))
+        p_o.append(H.to_np_bits(p0, "f32").view(np.float32))
+        del p0
+        assert adam.add_layer_params(idx, [params[idx]]) == idx
+    # layer 0 is not the last one: its moments went to their files at registration
+    assert adam.exp_avg_flat[0].untyped_storage().nbytes() == 0
+    m_o = [np.zeros(n, np.float32) for n in sizes]
+    v_o = [np.zeros(n, np.float32) for n in sizes]
+    orc = O.OracleAdam(6e-6, (0.9, 0.999), 1e-8, 0.01, True)
+    for it in range(2):
+        for idx in (1, 0):                                   # sliding order: the last layer first
+            n = sizes[idx]
+            log(f"NVMe C5: iteration {it}, layer {idx} ({n} params)")
+            g = device_randn(n, 13000 + 10 * it + idx, dev, 5e-4).bfloat16()
+            group = adam.begin_chunk_step(idx)
+            assert adam.exp_avg_flat[idx].untyped_storage().nbytes() == 4 * n     # read back (prefetched)
+            adam.step_chunk(params[idx].data, g, adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx], group)
+            adam.end_chunk_step(idx)
+            orc.update(group["step"], 6e-6, 0.9, 0.999, 1e-8, 0.01, True, p_o[idx], H.to_np_bits(g, "bf16"),
+                       m_o[idx], v_o[idx], g16="bf16")
+            del g
+    adam.offloader.sync_write_events()
+    # the C5 layer's moments were written back last and released; the small
+    # layer's last release was cancelled by the prefetch that followed it (its
+    # write was fenced), so its buffers still hold the bytes: write them out
+    assert adam.exp_avg_flat[0].untyped_storage().nbytes() == 0
+    for idx, n in enumerate(sizes):
+        log(f"NVMe C5: layer {idx} against the CPU checker")
+        bad = np.flatnonzero(params[idx].data.numpy().view(np.uint32) != p_o[idx].view(np.uint32))[:8]
+        assert bad.size == 0, (idx, "p", bad)
+        for t in (adam.exp_avg_flat[idx], adam.exp_avg_sq_flat[idx]):
+            if t.untyped_storage().nbytes():
+                adam.offloader.sync_write(t)
+            assert t.untyped_storage().nbytes() == 0                              # in its file only
+        adam._load_layer(idx)
+        adam.offloader.sync_read_events()
+        for t, want, what in ((adam.exp_avg_flat[idx], m_o[idx], "m"), (adam.exp_avg_sq_flat[idx], v_o[idx], "v")):
+            bad = np.flatnonzero(t.numpy().view(np.uint32) != want.view(np.uint32))[:8]
+            assert bad.size == 0, (idx, what, bad)
+    del adam, params, p_o, m_o, v_o
