@@ -1,9 +1,9 @@
 """Child process of tests/test_gpu_allocators.py (not a test module).
 
 Runs LayerAdam on one GPU under whatever torch caching-allocator
-configuration the parent put into PYTORCH_HIP_ALLOC_CONF (expandable
-segments, the stream-ordered hipMallocAsync backend, or the default), so that
-every device array the library sees comes from that allocator:
+configuration the parent put into PYTORCH_HIP_ALLOC_CONF (the stream-ordered
+hipMallocAsync backend, or the default), so that every device array the
+library sees comes from that allocator:
   A. clip_grad_norm over three device grads, then step_with_grad_views twice
      with the clip coefficient (la_grad_norm_multi, la_adam_update_multi);
   B. step_chunk on flat device buffers with the bf16 copy (la_adam_update);
