@@ -353,6 +353,8 @@ class LayerAdam:
             overlap_host_chunks: bool = False,
             moments_device: Optional[torch.device] = None,
             moments_hbm_bytes: Optional[int] = None,
+            stream_chunk_elems: int = HOST_STAGE_ELEMS,
+            stream_slots: int = HOST_STAGE_SLOTS,
     ):
         """Arguments of the reference (layer_adam.py:17-30), plus keyword-only:
         ``device``: the HIP device that updates host-resident state (default: current);
@@ -376,7 +378,15 @@ class LayerAdam:
         passed in, host and device alike (grads, moments in HBM, ``bf16_out``,
         ``clip_coef``), must not be read or written by the caller; the optimizer
         keeps a reference to each of them until its update is complete, so a
-        temporary the caller drops is not freed early."""
+        temporary the caller drops is not freed early;
+        ``stream_chunk_elems``, ``stream_slots``: the chunk (elements, rounded
+        down to a multiple of 16) and the number of device staging slots with
+        which host-resident arrays stream through HBM.  The defaults, 16 Mi
+        elements (64 MB of fp32) and 3 slots, are the best or near it for
+        every measured layout but one: a page-locked master with the moments in
+        HBM in one call of a very large layer (1.8 B params), where 64 Mi x 3
+        runs 150 ms against 180-207 ms (64 MB copies back to the host then go
+        partly to a DMA engine that the other direction also uses)."""
         self.defaults = dict(
             lr=lr,
             bias_correction=bias_correction,
@@ -393,6 +403,8 @@ class LayerAdam:
                              "the file offload moves host-resident moments")
         if moments_hbm_bytes is not None and (moments_device is None or moments_hbm_bytes < 0):
             raise ValueError("moments_hbm_bytes needs moments_device and must be >= 0")
+        if int(stream_chunk_elems) < 16 or not 1 <= int(stream_slots) <= 16:
+            raise ValueError("stream_chunk_elems must be at least 16 and stream_slots 1..16")
 
         # The reference loads its CPU extension here (layer_adam.py:59); this
         # loads the HIP library and fails loudly if it is missing.  cpu_adam is
@@ -414,6 +426,8 @@ class LayerAdam:
         self.overlap_host_chunks = overlap_host_chunks
         self.moments_device = torch.device(moments_device) if moments_device is not None else None
         self.moments_hbm_bytes = moments_hbm_bytes
+        self.stream_chunk_elems = int(stream_chunk_elems)
+        self.stream_slots = int(stream_slots)
         self.moments_hbm_used = 0     # bytes of moments placed on moments_device so far
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
 
@@ -672,7 +686,8 @@ class LayerAdam:
         with torch.cuda.device(device):
             streamer = self._streamers.get(device)
             if streamer is None:
-                streamer = self._streamers[device] = HostStreamer(device)
+                streamer = self._streamers[device] = HostStreamer(device, chunk_elems=self.stream_chunk_elems,
+                                                                  slots=self.stream_slots)
             on_host = _placement(params, grads, exp_avg, exp_avg_sq, bf16_out)
             self.last_stream_stats = streamer.step(
                 sc, pc, params, gc, grads, sc_, exp_avg, exp_avg_sq, n, bf16_out, on_host,

@@ -1246,6 +1246,30 @@ def test_streamed_call_beyond_2_pow_32_elements(hip_device):
     torch.cuda.empty_cache()
 
 
+def test_stream_shape_options_set_the_pipeline(hip_device):
+    """LayerAdam(stream_chunk_elems=, stream_slots=) streams host arrays in
+    chunks of that size: 20,013 elements at 4096 take 5 chunks (the last one
+    short, holding the scalar tail), bit-exact with the CPU checker."""
+    n, chunk = 20_013, 4096
+    rng = np.random.default_rng(77)
+    p_h = rng.normal(0, 0.02, n).astype(np.float32)
+    g_h = O.f32_to_bf16(rng.normal(0, 1e-3, n).astype(np.float32))
+    adam = LayerAdam(lr=1e-3, weight_decay=0.01, stream_chunk_elems=chunk, stream_slots=2)
+    p = torch.from_numpy(p_h.copy())
+    m, v = torch.zeros(n), torch.zeros(n)
+    g = torch.from_numpy(g_h.view(np.int16).copy()).view(torch.bfloat16)
+    adam.step_chunk(p, g, m, v, dict(adam.defaults, step=1))
+    st = adam.last_stream_stats
+    assert st.chunks == 5 and st.h2d_bytes == 14 * n
+    assert adam._streamers[hip_device].chunk == chunk and adam._streamers[hip_device].slots == 2
+    m_h, v_h = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    O.OracleAdam(1e-3, (0.9, 0.999), 1e-8, 0.01, True).update(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, p_h, g_h, m_h,
+                                                              v_h, g16="bf16")
+    assert np.array_equal(p.numpy().view(np.uint32), p_h.view(np.uint32))
+    assert np.array_equal(m.numpy().view(np.uint32), m_h.view(np.uint32))
+    assert np.array_equal(v.numpy().view(np.uint32), v_h.view(np.uint32))
+
+
 def test_pipeline_rejects_bad_arguments_before_any_transfer(hip_device):
     """la_pipeline_step validates the dtype triple, device-pointer alignment,
     placement and the current device up front: the host state is left

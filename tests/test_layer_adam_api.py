@@ -21,6 +21,17 @@ def test_constructor_defaults_match_reference():
     assert adam.fp32_optimizer_state is True and adam.num_layer == 0 and adam.pin_memory is False
 
 
+def test_stream_shape_options():
+    """Keyword-only additions: the chunk and slots host arrays stream with."""
+    adam = LayerAdam()
+    assert adam.stream_chunk_elems == 16 * 1024 * 1024 and adam.stream_slots == 3
+    adam = LayerAdam(stream_chunk_elems=64 * 1024 * 1024, stream_slots=2)
+    assert adam.stream_chunk_elems == 64 * 1024 * 1024 and adam.stream_slots == 2
+    for bad in (dict(stream_chunk_elems=8), dict(stream_slots=0), dict(stream_slots=17)):
+        with pytest.raises(ValueError, match="stream_chunk_elems"):
+            LayerAdam(**bad)
+
+
 def test_unique_optimizer_ids():
     assert LayerAdam().optimizer_id != LayerAdam().optimizer_id
 
