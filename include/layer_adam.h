@@ -198,7 +198,7 @@ int la_grad_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, voi
  * Stage 1 of this build never uses more than 256 workgroups, so every n fits;
  * a build whose stage-1 grid could outgrow the array returns LA_ERANGE for
  * such n.  Runs on the current device; `stream` must belong to it (NULL and
- * the per-thread default stream do): a stream of another device is refused
+ * the legacy and per-thread default streams do): a stream of another device is refused
  * with LA_EINVAL before any launch.  Every
  * call on one GPU shares that GPU's array, which keeps the last call's
  * partials: calls that overlap on one GPU (streams not ordered with each

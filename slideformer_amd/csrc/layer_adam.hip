@@ -1180,6 +1180,8 @@ try {
     auto flush = [&]() -> int {
         if (batch.count == 0) return LA_OK;
         // one wave per run and per segment: the grid must fit the dispatch packet
+        // (holds by construction: a batch takes at most LA_MAX_GRID / 2 runs and
+        // kMaxSegs segments)
         if (runs + batch.count > static_cast<uint64_t>(LA_MAX_GRID)) return LA_EINVAL;
         batch.run_begin[batch.count] = runs;
         const int rc = dispatch_triple<MultiLauncher>(p_dtype, g_dtype, s_dtype, batch, runs + batch.count, st);
@@ -1251,8 +1253,9 @@ try {
     if (e != hipSuccess) return hip_rc(e);
     // the scratch address is the current device's: a stream of another device
     // would run the kernels there, on that device's memory
+    // NULL, the legacy and the per-thread default stream are the current device's
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (st != nullptr && st != hipStreamPerThread) {
+    if (st != nullptr && st != hipStreamPerThread && st != hipStreamLegacy) {
         hipDevice_t stream_dev = -1;
         e = hipStreamGetDevice(st, &stream_dev);
         if (e != hipSuccess) return hip_rc(e);

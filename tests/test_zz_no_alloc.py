@@ -107,8 +107,9 @@ def test_no_alloc_norm_on_a_side_stream_and_empty_input(hip_device):
 
 def test_no_alloc_norm_checks_the_stream_device(hip_device):
     """The fixed array's address is the current device's, so the stream must
-    belong to the current device: the default stream (NULL), the per-thread
-    default stream and a stream created on the current device are accepted,
+    belong to the current device: the default stream (NULL), the legacy and
+    the per-thread default stream and a stream created on the current device
+    are accepted,
     with the same bits as the workspace call; a stream of another device is
     refused with LA_EINVAL before any launch (needs a second GPU)."""
     L = _lib.load()
@@ -116,7 +117,8 @@ def test_no_alloc_norm_checks_the_stream_device(hip_device):
     zero = torch.zeros(1, dtype=torch.float64, device=hip_device)
     ref = _with_workspace(L, g, 0, zero, 1.0, torch.cuda.current_stream(hip_device).cuda_stream)
     own = torch.cuda.Stream(hip_device)
-    for name, st in (("NULL", None), ("per-thread", ctypes.c_void_p(2)), ("created", own.cuda_stream)):
+    for name, st in (("NULL", None), ("legacy", ctypes.c_void_p(1)), ("per-thread", ctypes.c_void_p(2)),
+                     ("created", own.cuda_stream)):
         print(f"no-alloc norm on the {name} stream", flush=True)
         got = _no_alloc(L, g, 0, zero, 1.0, st)
         for a, b in zip(got, ref):
