@@ -355,3 +355,82 @@ def test_library_of_another_abi_version_is_refused(tmp_path):
             _lib.load(str(so))
     finally:
         _lib._lib = saved
+
+
+def _header_prototypes():
+    """{name: (return kind, [parameter kinds])} of every function include/layer_adam.h declares.
+    Kinds: ptr, f32, f64, i32, u32, u64."""
+    text = re.sub(r"/\*.*?\*/", "", _read(HEADER), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    scalar = {"float": "f32", "double": "f64", "int": "i32", "int32_t": "i32", "unsigned": "u32",
+              "uint32_t": "u32", "uint64_t": "u64", "la_stream_t": "ptr"}
+
+    def kind(decl):
+        decl = decl.strip()
+        if "*" in decl:
+            return "ptr"
+        words = [w for w in decl.split() if w != "const"]
+        return scalar[words[0]]
+
+    out = {}
+    for ret, name, params in re.findall(r"^\s*(int|uint64_t|const char\*)\s+(la_\w+)\s*\(([^)]*)\)\s*;", text,
+                                        re.M | re.S):
+        params = [] if params.strip() == "void" else [kind(p) for p in params.split(",")]
+        out[name] = (kind(ret), params)
+    return out
+
+
+def _ctypes_kind(t):
+    if t in (ctypes.c_void_p, ctypes.c_char_p) or (isinstance(t, type) and issubclass(t, ctypes._Pointer)):
+        return "ptr"
+    return {ctypes.c_float: "f32", ctypes.c_double: "f64", ctypes.c_int: "i32", ctypes.c_uint: "u32",
+            ctypes.c_uint64: "u64"}[t]
+
+
+def test_binding_argtypes_follow_the_header():
+    """Every ctypes prototype of _lib (argument and return types) is the
+    header's, kind by kind: pointers, 32-bit ints, unsigned, 64-bit sizes and
+    floats in the same positions."""
+    L = _lib.load()
+    protos = _header_prototypes()
+    assert sorted(protos) == sorted(_lib.EXPORTED)
+    for name, (ret, params) in protos.items():
+        fn = getattr(L, name)
+        assert [_ctypes_kind(t) for t in fn.argtypes] == params, name
+        assert _ctypes_kind(fn.restype) == ret, name
+
+
+def test_struct_mirrors_match_the_c_layout(tmp_path):
+    """The ctypes mirrors of la_scalars_t, la_segment_t, la_grad_buffer_t and
+    la_pipeline_stats_t have the C compiler's size, field offsets and field
+    sizes (a C program built against the header prints them)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    mirrors = {"la_scalars_t": _lib.LaScalars, "la_segment_t": _lib.LaSegment,
+               "la_grad_buffer_t": _lib.LaGradBuffer, "la_pipeline_stats_t": _lib.LaPipelineStats}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "layer_adam.h"', "int main(void) {"]
+    for cname, S in mirrors.items():
+        lines.append(f'    printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in S._fields_:
+            lines.append(f'    printf("{cname} {field} %zu %zu\\n", offsetof({cname}, {field}), '
+                         f'sizeof((({cname}*)0)->{field}));')
+    lines += ["    return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = str(tmp_path / "layout")
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", exe],
+                   check=True)
+    got = {}
+    for line in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n"):
+        if line:
+            cname, field, *values = line.split()
+            got[(cname, field)] = tuple(int(v) for v in values)
+    for cname, S in mirrors.items():
+        assert got[(cname, "size")] == (ctypes.sizeof(S),), cname
+        for field, _ in S._fields_:
+            desc = getattr(S, field)
+            assert got[(cname, field)] == (desc.offset, desc.size), (cname, field)
