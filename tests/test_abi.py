@@ -434,3 +434,23 @@ def test_struct_mirrors_match_the_c_layout(tmp_path):
         for field, _ in S._fields_:
             desc = getattr(S, field)
             assert got[(cname, field)] == (desc.offset, desc.size), (cname, field)
+
+
+@pytest.mark.parametrize("entry", ["LayerAdam", "cpu_adam_compat"])
+def test_missing_library_fails_loudly(tmp_path, entry):
+    """Without the built HIP library both entry points of the drop-in raise
+    ImportError naming the build command: nothing falls back to a CPU path.
+    Run in a fresh process pointed at a library file that does not exist."""
+    import subprocess
+    import sys
+
+    code = {
+        "LayerAdam": "from slideformer_amd import LayerAdam\nLayerAdam()\n",
+        "cpu_adam_compat": ("from slideformer_amd import cpu_adam_compat\n"
+                            "cpu_adam_compat.create_adam(0, 1e-3, 0.9, 0.999, 1e-8, 0.0, True, False)\n"),
+    }[entry]
+    env = dict(os.environ, SLIDEFORMER_AMD_LIB=str(tmp_path / "missing.so"))
+    res = subprocess.run([sys.executable, "-c", code], env=env, cwd=REPO, capture_output=True, text=True,
+                         timeout=600)
+    assert res.returncode != 0
+    assert "ImportError" in res.stderr and "there is no CPU fallback" in res.stderr, res.stderr[-2000:]
