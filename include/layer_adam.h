@@ -193,8 +193,10 @@ int la_grad_norm_multi(int g_dtype, const la_grad_buffer_t* bufs, int count, voi
  * that forbid hipMalloc).  No counterpart in the reference.  The stage-1
  * partials go to a fixed device array inside the library of
  * LA_NORM_SCRATCH_PARTIALS float64 (2 KiB), one copy per GPU, held until the
- * process ends; its address is looked up once per device.  The call itself
- * allocates nothing (no hipMalloc, no hipFree, no allocating library call).
+ * process ends; its address is looked up once per device and kept in a fixed
+ * table of device ordinals 0-63 (a higher ordinal gives LA_EINVAL).  The call
+ * itself allocates nothing (no hipMalloc, no hipFree, no allocating library
+ * call, no host heap).
  * Stage 1 of this build never uses more than 256 workgroups, so every n fits;
  * a build whose stage-1 grid could outgrow the array returns LA_ERANGE for
  * such n.  Runs on the current device; `stream` must belong to it (NULL and

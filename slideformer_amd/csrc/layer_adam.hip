@@ -1019,23 +1019,26 @@ namespace {
 
 constexpr uint64_t kScratchBytes = static_cast<uint64_t>(LA_NORM_SCRATCH_PARTIALS) * sizeof(double);
 
+// Device ordinals the address table covers; a fixed table, so that not even
+// the first call on a device allocates host memory.
+constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
-std::unordered_map<int, double*> g_scratch_ptr;  // device ordinal -> that device's copy of `scratch`
+double* g_scratch_ptr[kScratchDevices] = {};  // device ordinal -> that device's copy of `scratch`
 
 // The address of `scratch` on device `dev`, which is the current device,
 // looked up once per device with that device current.
 int scratch_on_current_device(int dev, double** out)
 {
+    if (dev < 0 || dev >= kScratchDevices) return LA_EINVAL;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    auto it = g_scratch_ptr.find(dev);
-    if (it == g_scratch_ptr.end()) {
+    if (!g_scratch_ptr[dev]) {
         void* ptr = nullptr;
         const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_rc(e);
         if (!ptr) return LA_EINVAL;
-        it = g_scratch_ptr.emplace(dev, static_cast<double*>(ptr)).first;
+        g_scratch_ptr[dev] = static_cast<double*>(ptr);
     }
-    *out = it->second;
+    *out = g_scratch_ptr[dev];
     return LA_OK;
 }
 
